@@ -1,0 +1,125 @@
+/*
+ * taomate_h3_amd -- C ABI of the MI355X (gfx950) quantized-linear library.
+ *
+ * Drop-in native boundary for TaoMate-H3's W8A8 linear path.  Every entry
+ * point is stateless and reentrant: it takes raw device pointers, element or
+ * byte strides, sizes and a hipStream_t (passed as void*; NULL = the legacy
+ * default stream), enqueues its kernels on that stream and returns without
+ * synchronising.  Nothing here allocates device memory; buffers belong to the
+ * caller.  A non-zero return is an error code; h3q_last_error() then returns
+ * a message (thread-local, valid until the next call on the same thread).
+ * Argument errors are detected on the host before any launch.
+ *
+ * Data conventions: bf16 and e4m3fn values are raw bit patterns (uint16_t /
+ * uint8_t); matrices are row-major with the given leading dimension.
+ */
+#ifndef TAOMATE_H3_AMD_H
+#define TAOMATE_H3_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Code formats. */
+#define H3Q_FMT_E4M3FN 0 /* OCP float8 e4m3fn, largest finite 448 */
+#define H3Q_FMT_INT8 1   /* symmetric int8 */
+
+/* Rounding forms of the per-row quantizer. */
+#define H3Q_ROUND_DIV 0     /* q = round(x / s), s = max(amax / L, 1e-12)  (reference weight quantizer) */
+#define H3Q_ROUND_RCP_MUL 1 /* q = sat8(rint(x * (127 / amax))), s = amax / 127  (vLLM dynamic int8) */
+
+/* Scale granularities of the scaled GEMM. */
+#define H3Q_SCALE_PER_TENSOR 0 /* one fp32 value */
+#define H3Q_SCALE_PER_ROW 1    /* a: one per token (row of A); b: one per output channel (row of B) */
+
+/* Status codes. */
+#define H3Q_OK 0
+#define H3Q_ERR_INVALID 1     /* bad argument (checked before any launch) */
+#define H3Q_ERR_UNSUPPORTED 2 /* valid request this build does not implement */
+#define H3Q_ERR_HIP 3         /* the HIP runtime refused a launch */
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int h3q_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* h3q_last_error(void);
+
+/*
+ * Per-row dynamic quantization of a bf16 matrix x [rows, cols] (leading
+ * dimension ldx elements) into codes [rows, cols] (leading dimension ldq
+ * bytes) and fp32 scales [rows].
+ *
+ *   format=E4M3FN, rounding=DIV : s = max(amax/448, 1e-12), q = e4m3(clamp(x/s, +-448))
+ *   format=INT8,   rounding=DIV : s = max(amax/127, 1e-12), q = clamp(rne(x/s), +-127)
+ *   format=INT8,   rounding=RCP_MUL : s = amax/127, q = sat8(rne(x * (127/amax))), zero row -> 0
+ *
+ * Replaces vLLM torch.ops._C.dynamic_scaled_int8_quant(out, in, scales, None)
+ * (called at H3/inference/w8a8.py:178 and, allocating, :212) with RCP_MUL,
+ * and the weight quantizer _quantize_weight (H3/inference/w8a8.py:57-63;
+ * FL/inference/w8a8.py:242-257) with INT8+DIV, applied to any row range so the
+ * 8 MiB streamed loader (H3/inference/w8a8.py:98-133) keeps its chunking.
+ * E4M3FN+DIV is the per-token / per-output-channel FP8 quantizer.
+ */
+int h3q_quant_rows(const void* x, int64_t rows, int64_t cols, int64_t ldx, int format, int rounding,
+                   void* codes, int64_t ldq, float* scales, void* stream);
+
+/*
+ * Per-tensor e4m3fn quantization with a bf16 intermediate:
+ *   s = static_scale ? *static_scale : max(amax(|x|)/448, 1e-12)
+ *   q = e4m3(clamp(bf16(x / s), +-448));  *scale_out = s
+ * Replaces quantize_fp8_e4m3_dynamic / quantize_fp8_e4m3
+ * (FL/inference/fused_kernels.py:771-820) and the per-tensor FP8 weight
+ * quantizer (FL/inference/fp8.py:259-263, :107-113).  `partial` is caller
+ * workspace of h3q_quant_tensor_workspace_floats(rows, cols) floats (unused
+ * when static_scale is given).  Two kernels: partial maxima, then quantize.
+ */
+int64_t h3q_quant_tensor_workspace_floats(int64_t rows, int64_t cols);
+int h3q_quant_tensor_e4m3(const void* x, int64_t rows, int64_t cols, int64_t ldx, const float* static_scale,
+                          float* partial, void* codes, int64_t ldq, float* scale_out, void* stream);
+
+/*
+ * Scaled GEMM with fused epilogue:
+ *   out[m, n] = bf16( a_scale[m] * (b_scale[n] * float(sum_k a[m, k] * b[n, k])) [+ bias[n]]
+ *                     [+ lora_scale * sum_r lora_t[m, r] * lora_b[n, r]] )
+ * a: codes [m, k] (lda bytes), b: weight codes [n, k] (ldb bytes, the
+ * nn.Linear layout, i.e. cutlass_scaled_mm's B = weight.t()), format E4M3FN
+ * or INT8 for both.  a_scale_kind / b_scale_kind: H3Q_SCALE_PER_ROW or
+ * H3Q_SCALE_PER_TENSOR.  bias: bf16 [n] or NULL (added as one fused
+ * multiply-add: fma(a_scale, b_scale * acc, bias)).  lora_t: bf16 [m, rank]
+ * (ldt elements) = x @ lora_a^T, lora_b: bf16 [n, rank] (ldlb elements), or
+ * both NULL; rank <= 128 and a multiple of 8.  out: bf16 [m, n] (ldo elements).
+ * Requires k % 16 == 0, lda and ldb multiples of 16 bytes, 16-byte aligned a/b.
+ * Replaces vLLM cutlass_scaled_mm (H3/inference/w8a8.py:179-186, :213-219)
+ * and torch._scaled_mm (FL/distributed/linear.py:92-100; FL/inference/fp8.py:135-143)
+ * plus the LoRA side branch (H3/inference/lora_checkpoint.py:196-205).
+ */
+int h3q_scaled_mm(int format, const void* a, int64_t lda, const float* a_scale, int a_scale_kind, const void* b,
+                  int64_t ldb, const float* b_scale, int b_scale_kind, const void* bias, const void* lora_t,
+                  int64_t ldt, const void* lora_b, int64_t ldlb, int64_t lora_rank, float lora_scale, void* out,
+                  int64_t ldo, int64_t m, int64_t n, int64_t k, void* stream);
+
+/*
+ * Raw int32 accumulators of the int8 GEMM: out[m, n] = sum_k a[m, k] * b[n, k]
+ * (a [m, k], b [n, k] int8; out int32, ldo elements).  Exposes the integer
+ * core of cutlass_scaled_mm (H3/inference/w8a8.py:179-186) for bit-exact
+ * checks.  Same layout requirements as h3q_scaled_mm.
+ */
+int h3q_gemm_i8_i32(const void* a, int64_t lda, const void* b, int64_t ldb, void* out, int64_t ldo, int64_t m,
+                    int64_t n, int64_t k, void* stream);
+
+/*
+ * LoRA down-projection t = bf16(x @ lora_a^T): x bf16 [m, k] (ldx elements),
+ * lora_a bf16 [rank, k] (lda elements), t bf16 [m, rank] (ldt elements).
+ * The first F.linear of H3/inference/lora_checkpoint.py:197-199, whose bf16
+ * result feeds h3q_scaled_mm's fused LoRA epilogue.  k % 8 == 0.
+ */
+int h3q_lora_down(const void* x, int64_t ldx, const void* lora_a, int64_t lda, void* t, int64_t ldt, int64_t m,
+                  int64_t k, int64_t rank, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TAOMATE_H3_AMD_H */

@@ -1,0 +1,274 @@
+/*
+ * CPU oracle for the quantized-linear path.  TEST INFRASTRUCTURE ONLY: this
+ * library is loaded by tests/, by __graft_entry__.smoke() as the checker and by
+ * bench.py's cpu_baseline leg.  The product path never links or calls it.
+ *
+ * It restates, in plain C with IEEE single/double arithmetic, the arithmetic of
+ * the reference's quantizers and scaled GEMMs:
+ *
+ *   orc_quant_rows_int8_div    H3/inference/w8a8.py:57-63 (_quantize_weight)
+ *                              FL/inference/w8a8.py:242-257 (same formula)
+ *   orc_quant_rows_e4m3_div    per-token / per-channel e4m3fn: the formula of
+ *                              w8a8.py:57-63 with 127 -> 448 and the e4m3fn cast,
+ *                              fp32 quotient as in FL/inference/fused_kernels.py:826-834
+ *   orc_quant_rows_int8_rcp    vLLM 0.11.1 dynamic_scaled_int8_quant semantics
+ *                              (called at H3/inference/w8a8.py:178); third-party,
+ *                              parity unpinned against vLLM itself
+ *   orc_quant_tensor_e4m3      FL/inference/fused_kernels.py:771-796 (eager) and
+ *                              :140-172,230-247 (Triton: bf16 intermediate);
+ *                              FL/inference/fp8.py:259-263 (weights)
+ *   orc_gemm_i8_i32            exact int32 accumulators of cutlass_scaled_mm
+ *                              (H3/inference/w8a8.py:179-186)
+ *   orc_gemm_e4m3_f64          exact real value of an e4m3 x e4m3 dot product
+ *                              (products exact, sums exact in binary64 for K <= 2^20)
+ *   orc_epilogue_*             s_a * (s_w * float(acc)) [+ bias] -> bf16 RNE
+ *
+ * The e4m3fn and bf16 encoders are written from the format definitions (RNE on
+ * an exact binary64 value); they are checked against torch's casts by the tests.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#define ORC_API __attribute__((visibility("default")))
+
+static float f32_from_bits(uint32_t b) { float f; memcpy(&f, &b, 4); return f; }
+static uint32_t bits_from_f32(float f) { uint32_t b; memcpy(&b, &f, 4); return b; }
+
+/* ------------------------------------------------------------------ bf16 */
+
+ORC_API float orc_bf16_to_f32(uint16_t h) { return f32_from_bits((uint32_t)h << 16); }
+
+/* Round a binary32 value to bfloat16 (round to nearest, ties to even).  The
+ * rounding is done on the exact binary64 value: bfloat16 keeps 8 significant
+ * bits and the binary32 exponent range, so the quantum is 2^(e-7) for a value
+ * with exponent e >= -126 and 2^-133 below. */
+ORC_API uint16_t orc_f32_to_bf16(float f) {
+    uint32_t b = bits_from_f32(f);
+    if (isnan(f)) return (uint16_t)((b >> 16) | 0x40);   /* quiet NaN, sign kept */
+    if (isinf(f) || f == 0.0f) return (uint16_t)(b >> 16);
+    double a = fabs((double)f);
+    int e;
+    frexp(a, &e);                 /* a = m * 2^e, m in [0.5,1) -> exponent e-1 */
+    int ex = e - 1;
+    if (ex < -126) ex = -126;
+    double quantum = ldexp(1.0, ex - 7);
+    double r = nearbyint(a / quantum) * quantum;   /* exact: power-of-two scaling */
+    float rf = (float)r;                           /* exact or overflow to inf */
+    uint32_t rb = bits_from_f32(rf) | (b & 0x80000000u);
+    return (uint16_t)(rb >> 16);
+}
+
+/* ---------------------------------------------------------------- e4m3fn */
+
+/* OCP float8 e4m3fn: 1 sign, 4 exponent (bias 7), 3 mantissa bits, no
+ * infinities, S.1111.111 is NaN, largest finite 448, smallest subnormal 2^-9. */
+ORC_API float orc_e4m3_to_f32(uint8_t c) {
+    int s = c >> 7, e = (c >> 3) & 15, m = c & 7;
+    if (e == 15 && m == 7) return NAN;
+    double v = (e == 0) ? ldexp((double)m, -9) : ldexp(1.0 + m / 8.0, e - 7);
+    return (float)(s ? -v : v);
+}
+
+/* Round to nearest, ties to even, onto the e4m3fn grid.  A magnitude that
+ * rounds above 448 has no finite encoding and becomes NaN (0x7F), matching
+ * torch's float -> float8_e4m3fn cast (464 rounds to 448, 470 to NaN). */
+ORC_API uint8_t orc_f32_to_e4m3(float f) {
+    uint8_t sign = (uint8_t)((bits_from_f32(f) >> 24) & 0x80);
+    if (isnan(f)) return (uint8_t)(sign | 0x7F);
+    double a = fabs((double)f);
+    if (isinf(f)) return (uint8_t)(sign | 0x7F);
+    if (a == 0.0) return sign;
+    int e;
+    frexp(a, &e);
+    int ex = e - 1;                 /* a in [2^ex, 2^(ex+1)) */
+    if (ex < -6) ex = -6;           /* subnormal quantum 2^-9 */
+    double quantum = ldexp(1.0, ex - 3);
+    double r = nearbyint(a / quantum) * quantum;
+    if (r > 448.0) return (uint8_t)(sign | 0x7F);
+    if (r == 0.0) return sign;
+    uint8_t code;
+    if (r < ldexp(1.0, -6)) {
+        code = (uint8_t)(r / ldexp(1.0, -9));          /* 1..7 */
+    } else {
+        int er;
+        double mr = frexp(r, &er);                     /* r = mr*2^er, mr in [0.5,1) */
+        int expo = er - 1;                             /* r in [2^expo, 2^(expo+1)) */
+        int mant = (int)((mr * 2.0 - 1.0) * 8.0);      /* exact: 3 bits */
+        code = (uint8_t)(((expo + 7) << 3) | mant);
+    }
+    return (uint8_t)(sign | code);
+}
+
+/* ------------------------------------------------------ row quantization */
+
+static const float kE4M3Max = 448.0f;
+static const float kInt8Max = 127.0f;
+static const float kScaleFloor = 1.0e-12f;   /* torch.clamp(min=1.0e-12) on fp32 */
+
+static float row_amax(const uint16_t* x, int64_t k) {
+    float amax = 0.0f;
+    for (int64_t j = 0; j < k; ++j) {
+        float v = fabsf(orc_bf16_to_f32(x[j]));
+        if (v > amax || isnan(v)) amax = v;
+    }
+    return amax;
+}
+
+/* H3/inference/w8a8.py:57-63:
+ *   scale = clamp(amax_row(|W|).float() / 127, min=1e-12)
+ *   q     = int8(clamp(round_half_even(float(W) / scale), -127, 127))
+ * bf16 [rows,K] / fp32 [rows,1] promotes to fp32, so the quotient is one
+ * correctly rounded binary32 division. */
+ORC_API void orc_quant_rows_int8_div(const uint16_t* x, int64_t rows, int64_t k, int64_t ldx,
+                                     int8_t* q, int64_t ldq, float* scales) {
+    for (int64_t i = 0; i < rows; ++i) {
+        const uint16_t* xr = x + i * ldx;
+        float s = row_amax(xr, k) / kInt8Max;
+        if (s < kScaleFloor) s = kScaleFloor;
+        scales[i] = s;
+        for (int64_t j = 0; j < k; ++j) {
+            float v = nearbyintf(orc_bf16_to_f32(xr[j]) / s);
+            if (v < -127.0f) v = -127.0f;
+            if (v > 127.0f) v = 127.0f;
+            q[i * ldq + j] = (int8_t)v;
+        }
+    }
+}
+
+/* Per-row e4m3fn with an fp32 quotient:
+ *   scale = clamp(amax_row / 448, min=1e-12);  q = e4m3(clamp(float(x)/scale, +-448)) */
+ORC_API void orc_quant_rows_e4m3_div(const uint16_t* x, int64_t rows, int64_t k, int64_t ldx,
+                                     uint8_t* q, int64_t ldq, float* scales) {
+    for (int64_t i = 0; i < rows; ++i) {
+        const uint16_t* xr = x + i * ldx;
+        float s = row_amax(xr, k) / kE4M3Max;
+        if (s < kScaleFloor) s = kScaleFloor;
+        scales[i] = s;
+        for (int64_t j = 0; j < k; ++j) {
+            float v = orc_bf16_to_f32(xr[j]) / s;
+            if (v < -kE4M3Max) v = -kE4M3Max;
+            if (v > kE4M3Max) v = kE4M3Max;
+            q[i * ldq + j] = orc_f32_to_e4m3(v);
+        }
+    }
+}
+
+/* vLLM dynamic per-token int8 (third-party semantics, v0.11.1):
+ *   scale = amax / 127 (no floor); inv = amax == 0 ? 0 : 127 / amax
+ *   q = saturate_int8(round_half_even(float(x) * inv))
+ * The saturating convert maps NaN to 0 and +-inf to 127 / -128 (CUDA's
+ * cvt.rni.sat.s8.f32); NaN and inf arise when amax < 127 / FLT_MAX, where
+ * inv overflows and 0 * inv is NaN. */
+ORC_API void orc_quant_rows_int8_rcp(const uint16_t* x, int64_t rows, int64_t k, int64_t ldx,
+                                     int8_t* q, int64_t ldq, float* scales) {
+    for (int64_t i = 0; i < rows; ++i) {
+        const uint16_t* xr = x + i * ldx;
+        float amax = row_amax(xr, k);
+        scales[i] = amax / kInt8Max;
+        float inv = (amax == 0.0f) ? 0.0f : kInt8Max / amax;
+        for (int64_t j = 0; j < k; ++j) {
+            float v = nearbyintf(orc_bf16_to_f32(xr[j]) * inv);
+            if (isnan(v)) v = 0.0f;
+            if (v < -128.0f) v = -128.0f;
+            if (v > 127.0f) v = 127.0f;
+            q[i * ldq + j] = (int8_t)v;
+        }
+    }
+}
+
+/* Per-tensor e4m3fn (FL/inference/fused_kernels.py:771-796, fp8.py:259-263):
+ *   scale = clamp(amax_all.float() / 448, min=1e-12)      (0-dim fp32)
+ *   q = e4m3(clamp(bf16(float(x) / scale), +-448))
+ * A bf16 tensor divided by a 0-dim fp32 tensor yields bf16, so the binary32
+ * quotient is rounded to bf16 before the e4m3 cast (the Triton kernel's
+ * _round_bf16(div_rn(x, s))).  static_scale (nullable) replaces the dynamic
+ * scale as in quantize_fp8_e4m3(value, scale). */
+ORC_API void orc_quant_tensor_e4m3(const uint16_t* x, int64_t rows, int64_t k, int64_t ldx,
+                                   const float* static_scale, uint8_t* q, int64_t ldq,
+                                   float* scale_out) {
+    float s;
+    if (static_scale) {
+        s = *static_scale;
+    } else {
+        float amax = 0.0f;
+        for (int64_t i = 0; i < rows; ++i) {
+            float a = row_amax(x + i * ldx, k);
+            if (a > amax || isnan(a)) amax = a;
+        }
+        s = amax / kE4M3Max;
+        if (s < kScaleFloor) s = kScaleFloor;
+    }
+    *scale_out = s;
+    for (int64_t i = 0; i < rows; ++i) {
+        for (int64_t j = 0; j < k; ++j) {
+            float v = orc_bf16_to_f32(orc_f32_to_bf16(orc_bf16_to_f32(x[i * ldx + j]) / s));
+            if (v < -kE4M3Max) v = -kE4M3Max;
+            if (v > kE4M3Max) v = kE4M3Max;
+            q[i * ldq + j] = orc_f32_to_e4m3(v);
+        }
+    }
+}
+
+/* ----------------------------------------------------------------- GEMMs */
+
+/* acc[m][n] = sum_k a[m][k] * b[n][k], exact in int32 (|acc| <= K*128^2). */
+ORC_API void orc_gemm_i8_i32(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
+                             int32_t* c, int64_t ldc, int64_t m, int64_t n, int64_t k) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            int64_t acc = 0;
+            const int8_t* ar = a + i * lda;
+            const int8_t* br = b + j * ldb;
+            for (int64_t t = 0; t < k; ++t) acc += (int32_t)ar[t] * (int32_t)br[t];
+            c[i * ldc + j] = (int32_t)acc;
+        }
+}
+
+/* Exact real value of sum_k e4m3(a[m][k]) * e4m3(b[n][k]).  Each product is a
+ * 4-bit by 4-bit significand product scaled by 2^[-18,17]; binary64 holds any
+ * sum of up to 2^20 of them without rounding (span < 53 bits). */
+ORC_API void orc_gemm_e4m3_f64(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb,
+                               double* c, int64_t ldc, int64_t m, int64_t n, int64_t k) {
+    float lut[256];
+    for (int i = 0; i < 256; ++i) lut[i] = orc_e4m3_to_f32((uint8_t)i);
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            double acc = 0.0;
+            const uint8_t* ar = a + i * lda;
+            const uint8_t* br = b + j * ldb;
+            for (int64_t t = 0; t < k; ++t) acc += (double)lut[ar[t]] * (double)lut[br[t]];
+            c[i * ldc + j] = acc;
+        }
+}
+
+/* out = bf16(s_a[m] * (s_w[n] * float(acc)) [+ bias[n]]).  With a bias the
+ * final step is one fused multiply-add (the CUTLASS ScaledEpilogueBias order). */
+ORC_API void orc_epilogue_i32(const int32_t* acc, int64_t ldacc, const float* s_a, int s_a_per_row,
+                              const float* s_w, int s_w_per_col, const uint16_t* bias,
+                              uint16_t* out, int64_t ldo, int64_t m, int64_t n) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            float sa = s_a[s_a_per_row ? i : 0];
+            float sw = s_w[s_w_per_col ? j : 0];
+            float t = sw * (float)acc[i * ldacc + j];
+            float v = bias ? fmaf(sa, t, orc_bf16_to_f32(bias[j])) : sa * t;
+            out[i * ldo + j] = orc_f32_to_bf16(v);
+        }
+}
+
+/* Same epilogue on an exact (binary64) accumulator rounded once to binary32. */
+ORC_API void orc_epilogue_f64(const double* acc, int64_t ldacc, const float* s_a, int s_a_per_row,
+                              const float* s_w, int s_w_per_col, const uint16_t* bias,
+                              uint16_t* out, int64_t ldo, int64_t m, int64_t n) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            float sa = s_a[s_a_per_row ? i : 0];
+            float sw = s_w[s_w_per_col ? j : 0];
+            float t = sw * (float)acc[i * ldacc + j];
+            float v = bias ? fmaf(sa, t, orc_bf16_to_f32(bias[j])) : sa * t;
+            out[i * ldo + j] = orc_f32_to_bf16(v);
+        }
+}

@@ -1,0 +1,271 @@
+"""CPU oracle for the quantized-linear path (TEST INFRASTRUCTURE ONLY).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this module, and only as the checker.  The product package
+never imports it.
+
+Thin numpy wrapper over ``liboracle_h3q.so`` (``h3q_oracle.c``), whose header
+cites the reference file:line each routine restates.  bf16 arrays are carried
+as ``uint16`` bit patterns and e4m3fn arrays as ``uint8`` codes.
+
+Parity pins (each checked in ``tests/test_oracle_pins.py``):
+
+* ``f32_to_bf16`` / ``f32_to_e4m3`` / ``e4m3_to_f32``: against torch's casts
+  over every bf16 bit pattern and a random binary32 sample.
+* ``quant_rows(..., 'int8', 'div')``: against the reference expression of
+  ``H3/inference/w8a8.py:57-63`` evaluated by torch on CPU, plus closed-form
+  special cases (zero row, argmax -> +-127, ties to even).
+* ``quant_rows(..., 'e4m3', 'div')``: against the same expression with
+  127 -> 448 and torch's e4m3fn cast; special cases.
+* ``quant_tensor_e4m3``: against ``FL/inference/fused_kernels.py:771-796``'s
+  eager expression evaluated by torch (bf16 intermediate), special cases.
+* ``quant_rows(..., 'int8', 'rcp')``: vLLM semantics (third-party, absent):
+  pinned only by invariants -- parity unpinned against vLLM itself.
+* ``gemm_i8_i32``: against ``torch._int_mm`` and brute force.
+* ``gemm_e4m3_exact``: against binary64 matmul of decoded codes (exact) and
+  a hand-computed case.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "liboracle_h3q.so"
+_lib = None
+
+_i64 = ctypes.c_int64
+_p = ctypes.c_void_p
+
+
+def _load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not _LIB_PATH.exists():
+        subprocess.run(["make", "-C", str(_HERE)], check=True, capture_output=True)
+    lib = ctypes.CDLL(str(_LIB_PATH))
+    lib.orc_f32_to_bf16.restype = ctypes.c_uint16
+    lib.orc_f32_to_bf16.argtypes = [ctypes.c_float]
+    lib.orc_bf16_to_f32.restype = ctypes.c_float
+    lib.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.orc_f32_to_e4m3.restype = ctypes.c_uint8
+    lib.orc_f32_to_e4m3.argtypes = [ctypes.c_float]
+    lib.orc_e4m3_to_f32.restype = ctypes.c_float
+    lib.orc_e4m3_to_f32.argtypes = [ctypes.c_uint8]
+    for name in ("orc_quant_rows_int8_div", "orc_quant_rows_e4m3_div", "orc_quant_rows_int8_rcp"):
+        fn = getattr(lib, name)
+        fn.restype = None
+        fn.argtypes = [_p, _i64, _i64, _i64, _p, _i64, _p]
+    lib.orc_quant_tensor_e4m3.restype = None
+    lib.orc_quant_tensor_e4m3.argtypes = [_p, _i64, _i64, _i64, _p, _p, _i64, _p]
+    lib.orc_gemm_i8_i32.restype = None
+    lib.orc_gemm_i8_i32.argtypes = [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64]
+    lib.orc_gemm_e4m3_f64.restype = None
+    lib.orc_gemm_e4m3_f64.argtypes = [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64]
+    for name in ("orc_epilogue_i32", "orc_epilogue_f64"):
+        fn = getattr(lib, name)
+        fn.restype = None
+        fn.argtypes = [_p, _i64, _p, ctypes.c_int, _p, ctypes.c_int, _p, _p, _i64, _i64, _i64]
+    _lib = lib
+    return lib
+
+
+def _ptr(a: np.ndarray | None) -> int | None:
+    if a is None:
+        return None
+    return a.ctypes.data
+
+
+# ------------------------------------------------------------ scalar formats
+
+_E4M3_LUT: np.ndarray | None = None
+
+
+def e4m3_lut() -> np.ndarray:
+    """float32 value of each of the 256 e4m3fn codes (NaN for 0x7F/0xFF)."""
+    global _E4M3_LUT
+    if _E4M3_LUT is None:
+        lib = _load()
+        _E4M3_LUT = np.array([lib.orc_e4m3_to_f32(i) for i in range(256)], dtype=np.float32)
+    return _E4M3_LUT
+
+
+def e4m3_to_f32(codes: np.ndarray) -> np.ndarray:
+    return e4m3_lut()[np.asarray(codes, dtype=np.uint8)]
+
+
+def f32_to_e4m3(values: np.ndarray) -> np.ndarray:
+    lib = _load()
+    flat = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    out = np.fromiter((lib.orc_f32_to_e4m3(float(v)) for v in flat), dtype=np.uint8, count=flat.size)
+    return out.reshape(np.shape(values))
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(values: np.ndarray) -> np.ndarray:
+    lib = _load()
+    flat = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    out = np.fromiter((lib.orc_f32_to_bf16(float(v)) for v in flat), dtype=np.uint16, count=flat.size)
+    return out.reshape(np.shape(values))
+
+
+def f32_to_bf16_fast(values: np.ndarray) -> np.ndarray:
+    """Vectorised RNE binary32 -> bf16 for finite inputs (pinned against
+    ``f32_to_bf16`` in the tests); used for large arrays."""
+    b = np.ascontiguousarray(values, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    return rounded.astype(np.uint16)
+
+
+# ---------------------------------------------------------------- quantizers
+
+def quant_rows(x_bits: np.ndarray, fmt: str, rounding: str = "div") -> tuple[np.ndarray, np.ndarray]:
+    """Per-row quantization of a bf16 matrix (uint16 bits, shape [rows, K]).
+
+    fmt 'int8' + rounding 'div'  : H3/inference/w8a8.py:57-63
+    fmt 'int8' + rounding 'rcp'  : vLLM dynamic_scaled_int8_quant semantics
+    fmt 'e4m3' + rounding 'div'  : per-token / per-channel e4m3fn composition
+    Returns (codes [rows, K] int8|uint8, scales [rows] float32).
+    """
+    lib = _load()
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    rows, k = x.shape
+    scales = np.empty(rows, dtype=np.float32)
+    if fmt == "int8":
+        codes = np.empty((rows, k), dtype=np.int8)
+        fn = {"div": lib.orc_quant_rows_int8_div, "rcp": lib.orc_quant_rows_int8_rcp}[rounding]
+    elif fmt == "e4m3":
+        if rounding != "div":
+            raise ValueError("e4m3 rows use the division form only")
+        codes = np.empty((rows, k), dtype=np.uint8)
+        fn = lib.orc_quant_rows_e4m3_div
+    else:
+        raise ValueError(fmt)
+    fn(_ptr(x), rows, k, k, _ptr(codes), k, _ptr(scales))
+    return codes, scales
+
+
+def quant_tensor_e4m3(x_bits: np.ndarray, static_scale: float | None = None) -> tuple[np.ndarray, np.float32]:
+    """Per-tensor e4m3fn with the bf16 intermediate (FL/inference/fused_kernels.py:771-796)."""
+    lib = _load()
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    rows, k = x.shape
+    codes = np.empty((rows, k), dtype=np.uint8)
+    scale = np.zeros(1, dtype=np.float32)
+    st = None if static_scale is None else np.array([static_scale], dtype=np.float32)
+    lib.orc_quant_tensor_e4m3(_ptr(x), rows, k, k, _ptr(st), _ptr(codes), k, _ptr(scale))
+    return codes.reshape(np.shape(x_bits)), scale[0]
+
+
+# --------------------------------------------------------------------- GEMMs
+
+def gemm_i8_i32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Exact int32 acc[m, n] = sum_k a[m, k] * b[n, k]."""
+    lib = _load()
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    b = np.ascontiguousarray(b, dtype=np.int8)
+    m, k = a.shape
+    n = b.shape[0]
+    c = np.empty((m, n), dtype=np.int32)
+    lib.orc_gemm_i8_i32(_ptr(a), k, _ptr(b), k, _ptr(c), n, m, n, k)
+    return c
+
+
+def gemm_i8_i32_fast(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Exact int32 accumulators through an int64 BLAS-free matmul (numpy),
+    pinned against ``gemm_i8_i32`` in the tests; used for larger samples."""
+    return (a.astype(np.int64) @ b.astype(np.int64).T).astype(np.int32)
+
+
+def gemm_e4m3_exact(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Exact binary64 value of sum_k e4m3(a[m, k]) * e4m3(b[n, k])."""
+    lib = _load()
+    a = np.ascontiguousarray(a, dtype=np.uint8)
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    m, k = a.shape
+    n = b.shape[0]
+    c = np.empty((m, n), dtype=np.float64)
+    lib.orc_gemm_e4m3_f64(_ptr(a), k, _ptr(b), k, _ptr(c), n, m, n, k)
+    return c
+
+
+def gemm_e4m3_exact_fast(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Same exact value through a binary64 BLAS matmul.  Every partial sum is
+    a multiple of 2^-18 below 2^31, so binary64 represents each exactly and
+    summation order cannot change the result; pinned against the C loop."""
+    lut = e4m3_lut().astype(np.float64)
+    return lut[a] @ lut[b].T
+
+
+def epilogue(acc: np.ndarray, s_a: np.ndarray, s_w: np.ndarray, bias_bits: np.ndarray | None = None) -> np.ndarray:
+    """bf16 bits of s_a[m] * (s_w[n] * float(acc)) [+ bias[n] as one FMA].
+
+    ``acc`` int32 (int8 path) or float64 (exact fp8 sum, rounded once to
+    binary32).  ``s_a`` has M entries or 1 (per-tensor), ``s_w`` N or 1."""
+    lib = _load()
+    m, n = acc.shape
+    s_a = np.ascontiguousarray(np.ravel(s_a), dtype=np.float32)
+    s_w = np.ascontiguousarray(np.ravel(s_w), dtype=np.float32)
+    out = np.empty((m, n), dtype=np.uint16)
+    bias = None if bias_bits is None else np.ascontiguousarray(bias_bits, dtype=np.uint16)
+    if acc.dtype == np.int32:
+        acc = np.ascontiguousarray(acc)
+        fn = lib.orc_epilogue_i32
+    else:
+        acc = np.ascontiguousarray(acc, dtype=np.float64)
+        fn = lib.orc_epilogue_f64
+    fn(_ptr(acc), n, _ptr(s_a), int(s_a.size > 1), _ptr(s_w), int(s_w.size > 1), _ptr(bias),
+       _ptr(out), n, m, n)
+    return out
+
+
+# ------------------------------------------------------ float64 references
+
+def dequant_matmul_f64(q_a: np.ndarray, s_a: np.ndarray, q_w: np.ndarray, s_w: np.ndarray,
+                       fmt: str) -> np.ndarray:
+    """float64 value of the dequant-then-matmul path
+    F.linear(q_a.float() * s_a, q_w.float() * s_w) (FL/distributed/linear.py:92-100
+    semantics with row/col scales), before the bf16 rounding."""
+    if fmt == "e4m3":
+        acc = gemm_e4m3_exact_fast(q_a, q_w)
+    else:
+        acc = q_a.astype(np.float64) @ q_w.astype(np.float64).T
+    return acc * np.ravel(s_a).astype(np.float64)[:, None] * np.ravel(s_w).astype(np.float64)[None, :]
+
+
+def lora_reference(x_bits: np.ndarray, a_bits: np.ndarray, b_bits: np.ndarray, scale: float,
+                   base_bits: np.ndarray) -> np.ndarray:
+    """bf16 bits of output + update * scale with the rounding points of
+    H3/inference/lora_checkpoint.py:196-205:
+        t = bf16(x @ A^T); u = bf16(t @ B^T); out = bf16(base + bf16(u * scale))
+    Each matmul is evaluated in binary64 before its single bf16 rounding."""
+    x = bf16_to_f32(x_bits).astype(np.float64)
+    a = bf16_to_f32(a_bits).astype(np.float64)
+    b = bf16_to_f32(b_bits).astype(np.float64)
+    t = bf16_to_f32(f32_to_bf16_fast((x @ a.T).astype(np.float32))).astype(np.float64)
+    u = bf16_to_f32(f32_to_bf16_fast((t @ b.T).astype(np.float32)))
+    us = bf16_to_f32(f32_to_bf16_fast(u * np.float32(scale)))
+    base = bf16_to_f32(base_bits)
+    return f32_to_bf16_fast(base + us)
+
+
+def lora_down_reference(x_bits: np.ndarray, a_bits: np.ndarray) -> np.ndarray:
+    """float64 value of x @ A^T (before the bf16 rounding of t)."""
+    x = bf16_to_f32(x_bits).astype(np.float64)
+    a = bf16_to_f32(a_bits).astype(np.float64)
+    return x @ a.T
+
+
+def cpu_threads() -> int:
+    return os.cpu_count() or 1

@@ -1,0 +1,69 @@
+"""Build libtaomate_h3_amd.so (gfx950) from csrc/ with hipcc, in-tree.
+
+    python taomate-h3_amd/build.py
+
+The library exports only the C ABI of include/taomate_h3_amd.h.  Every HIP
+source is compiled for gfx950 with packed-FP32 instruction selection off.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libtaomate_h3_amd.so"
+SOURCES = ["act_quant.hip", "gemm.hip", "capi.hip"]
+
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build the gfx950 library)")
+
+
+def _quiet(text: str) -> str:
+    # hipcc's host pass does not know the GPU-only feature flag; drop that note.
+    return "\n".join(l for l in text.splitlines() if "packed-fp32-ops" not in l)
+
+
+def build(verbose: bool = False) -> Path:
+    objdir = PKG / "_build"
+    objdir.mkdir(exist_ok=True)
+    objects = []
+    cc = hipcc()
+    for src in SOURCES:
+        obj = objdir / (src + ".o")
+        cmd = [cc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src}:\n{_quiet(res.stderr)}")
+        if verbose and _quiet(res.stderr).strip():
+            print(_quiet(res.stderr), file=sys.stderr)
+        objects.append(str(obj))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [cc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *objects]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{_quiet(res.stderr)}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,292 @@
+// Per-row (per-token / per-output-channel) and per-tensor quantization of a
+// bf16 matrix to OCP e4m3fn or int8 codes, gfx950.
+//
+// Row kernel: one wavefront per row.  The whole row stays in VGPRs (NV 16-byte
+// vectors per lane, 64 lanes read 1 KiB contiguous per step), so X is read from
+// HBM exactly once: abs-max over packed bf16 bit patterns (v_pk_max_u16), a
+// butterfly wave reduction, one IEEE reciprocal per row, then a 3-op
+// correctly rounded quotient per element and 8-byte coalesced code stores.
+// Algorithmic traffic: 2*K read + K written + 4 bytes of scale per row.
+#include "h3q_common.hpp"
+#include "h3q_kernels.hpp"
+
+namespace h3q {
+
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_abs_max(uint32_t acc, uint32_t w) {
+    us2 a = __builtin_bit_cast(us2, acc);
+    us2 b = __builtin_bit_cast(us2, w & 0x7FFF7FFFu);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));
+}
+
+__device__ __forceinline__ float amax_from_packed(uint32_t m) {
+    uint32_t hi = m >> 16, lo = m & 0xFFFFu;
+    return __uint_as_float((hi > lo ? hi : lo) << 16);
+}
+
+// One row element -> code, for each quantizer form.
+template <int FMT, int ROUND>
+struct RowQuant {
+    float s, r;  // DIV: scale and RN(1/scale); RCP: scale and 127/amax
+    __device__ __forceinline__ void init(float amax) {
+        if (ROUND == kRoundRcpMul) {
+            s = amax / kInt8Max;
+            r = (amax == 0.0f) ? 0.0f : kInt8Max / amax;
+        } else {
+            s = row_scale(amax, FMT == kFmtE4M3 ? kE4M3Max : kInt8Max);
+            r = 1.0f / s;
+        }
+    }
+    __device__ __forceinline__ float value(float f) const {
+        if (ROUND == kRoundRcpMul) return __builtin_rintf(f * r);
+        float q = copysignf(div_rn(f, s, r), f);
+        return FMT == kFmtE4M3 ? q : __builtin_rintf(q);
+    }
+    // 4 bf16 (two packed words) -> 4 code bytes.
+    __device__ __forceinline__ uint32_t pack4(uint32_t w0, uint32_t w1) const {
+        float a = value(bf16_lo(w0)), b = value(bf16_hi(w0));
+        float c = value(bf16_lo(w1)), d = value(bf16_hi(w1));
+        if (FMT == kFmtE4M3) {
+            a = __builtin_amdgcn_fmed3f(a, -kE4M3Max, kE4M3Max);
+            b = __builtin_amdgcn_fmed3f(b, -kE4M3Max, kE4M3Max);
+            c = __builtin_amdgcn_fmed3f(c, -kE4M3Max, kE4M3Max);
+            d = __builtin_amdgcn_fmed3f(d, -kE4M3Max, kE4M3Max);
+            return cvt_e4m3x2(a, b) | (cvt_e4m3x2(c, d) << 16);
+        }
+        const float lo = (ROUND == kRoundRcpMul) ? -128.0f : -kInt8Max;
+        int ia = (int)__builtin_amdgcn_fmed3f(a, lo, kInt8Max);
+        int ib = (int)__builtin_amdgcn_fmed3f(b, lo, kInt8Max);
+        int ic = (int)__builtin_amdgcn_fmed3f(c, lo, kInt8Max);
+        int id = (int)__builtin_amdgcn_fmed3f(d, lo, kInt8Max);
+        return (uint32_t)(ia & 0xFF) | ((uint32_t)(ib & 0xFF) << 8) | ((uint32_t)(ic & 0xFF) << 16) |
+               ((uint32_t)id << 24);
+    }
+};
+
+// Vector path: K % 8 == 0, x rows 16-byte aligned, q rows 8-byte aligned, K <= NV*512.
+template <int FMT, int ROUND, int NV>
+__global__ __launch_bounds__(256) void quant_rows_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                             int64_t rows, int k, uint8_t* __restrict__ q,
+                                                             int64_t ldq, float* __restrict__ scales) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+    const int nvec = k >> 3;
+    uint4 v[NV];
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int vec = i * 64 + lane;
+        if (vec < nvec) {
+            v[i] = xr[vec];
+        } else {
+            v[i] = make_uint4(0, 0, 0, 0);
+        }
+        m = pk_abs_max(m, v[i].x);
+        m = pk_abs_max(m, v[i].y);
+        m = pk_abs_max(m, v[i].z);
+        m = pk_abs_max(m, v[i].w);
+    }
+    const float amax = wave_max(amax_from_packed(m));
+    RowQuant<FMT, ROUND> rq;
+    rq.init(amax);
+    uint2* qr = reinterpret_cast<uint2*>(q + row * ldq);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int vec = i * 64 + lane;
+        if (vec < nvec) {
+            uint2 out;
+            out.x = rq.pack4(v[i].x, v[i].y);
+            out.y = rq.pack4(v[i].z, v[i].w);
+            qr[vec] = out;
+        }
+    }
+    if (lane == 0) scales[row] = rq.s;
+}
+
+// General path (any K, any alignment): one workgroup per row, two passes.
+template <int FMT, int ROUND>
+__global__ __launch_bounds__(256) void quant_rows_any_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                             int64_t rows, int64_t k, uint8_t* __restrict__ q,
+                                                             int64_t ldq, float* __restrict__ scales) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const uint16_t* xr = x + row * ldx;
+    float amax = 0.0f;
+    for (int64_t j = threadIdx.x; j < k; j += 256) amax = fmaxf(amax, fabsf(bf16_lo(xr[j])));
+    amax = wave_max(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    RowQuant<FMT, ROUND> rq;
+    rq.init(amax);
+    for (int64_t j = threadIdx.x; j < k; j += 256) {
+        uint32_t w = xr[j];
+        q[row * ldq + j] = (uint8_t)(rq.pack4(w, 0u) & 0xFFu);
+    }
+    if (threadIdx.x == 0) scales[row] = rq.s;
+}
+
+template <int FMT, int ROUND, int NV>
+static hipError_t launch_rows_vec(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, uint8_t* q,
+                                  int64_t ldq, float* scales, hipStream_t st) {
+    const int64_t blocks = (rows + 3) / 4;
+    hipLaunchKernelGGL((quant_rows_vec_kernel<FMT, ROUND, NV>), dim3((unsigned)blocks), dim3(256), 0, st, x, ldx,
+                       rows, (int)k, q, ldq, scales);
+    return hipGetLastError();
+}
+
+template <int FMT, int ROUND>
+static hipError_t dispatch_rows(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, uint8_t* q, int64_t ldq,
+                                float* scales, hipStream_t st) {
+    const bool aligned = (k % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) &&
+                         ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
+    const int64_t nv = (k + 511) / 512;
+    if (aligned) {
+        if (nv <= 2) return launch_rows_vec<FMT, ROUND, 2>(x, ldx, rows, k, q, ldq, scales, st);
+        if (nv <= 4) return launch_rows_vec<FMT, ROUND, 4>(x, ldx, rows, k, q, ldq, scales, st);
+        if (nv <= 8) return launch_rows_vec<FMT, ROUND, 8>(x, ldx, rows, k, q, ldq, scales, st);
+        if (nv <= 12) return launch_rows_vec<FMT, ROUND, 12>(x, ldx, rows, k, q, ldq, scales, st);
+        if (nv <= 16) return launch_rows_vec<FMT, ROUND, 16>(x, ldx, rows, k, q, ldq, scales, st);
+        if (nv <= 24) return launch_rows_vec<FMT, ROUND, 24>(x, ldx, rows, k, q, ldq, scales, st);
+        if (nv <= 32) return launch_rows_vec<FMT, ROUND, 32>(x, ldx, rows, k, q, ldq, scales, st);
+    }
+    hipLaunchKernelGGL((quant_rows_any_kernel<FMT, ROUND>), dim3((unsigned)rows), dim3(256), 0, st, x, ldx, rows,
+                       k, q, ldq, scales);
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_rows(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, int fmt, int rounding,
+                             uint8_t* q, int64_t ldq, float* scales, hipStream_t st) {
+    if (fmt == kFmtE4M3) return dispatch_rows<kFmtE4M3, kRoundDiv>(x, ldx, rows, k, q, ldq, scales, st);
+    if (rounding == kRoundDiv) return dispatch_rows<kFmtInt8, kRoundDiv>(x, ldx, rows, k, q, ldq, scales, st);
+    return dispatch_rows<kFmtInt8, kRoundRcpMul>(x, ldx, rows, k, q, ldq, scales, st);
+}
+
+// ---------------------------------------------------------------- per-tensor
+
+// Pass 1: each workgroup reduces |x| over a contiguous band of rows.
+__global__ __launch_bounds__(256) void tensor_amax_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
+                                                          int64_t k, int64_t rows_per_block,
+                                                          float* __restrict__ partial) {
+    __shared__ float red[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+    const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
+    const bool vec = (k % 8 == 0) && (ldx % 8 == 0) && ((uintptr_t)x % 16 == 0);
+    uint32_t m = 0;
+    float amax = 0.0f;
+    for (int64_t r = r0 + wave; r < r1; r += 4) {
+        const uint16_t* xr = x + r * ldx;
+        if (vec) {
+            const uint4* xv = reinterpret_cast<const uint4*>(xr);
+            for (int64_t j = lane; j < (k >> 3); j += 64) {
+                uint4 v = xv[j];
+                m = pk_abs_max(m, v.x);
+                m = pk_abs_max(m, v.y);
+                m = pk_abs_max(m, v.z);
+                m = pk_abs_max(m, v.w);
+            }
+        } else {
+            for (int64_t j = lane; j < k; j += 64) amax = fmaxf(amax, fabsf(bf16_lo(xr[j])));
+        }
+    }
+    amax = wave_max(fmaxf(amax, amax_from_packed(m)));
+    if (lane == 0) red[wave] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// One element of the per-tensor quantizer: e4m3(clamp(bf16(x / s), +-448)).
+struct TensorQuant {
+    float s, r;
+    bool exact_div;  // static scale: plain IEEE division
+    __device__ __forceinline__ float value(float f) const {
+        float qv = exact_div ? __fdiv_rn(f, s) : copysignf(div_rn(f, s, r), f);
+        return __builtin_amdgcn_fmed3f(round_to_bf16(qv), -kE4M3Max, kE4M3Max);
+    }
+    __device__ __forceinline__ uint32_t pack4(uint32_t w0, uint32_t w1) const {
+        return cvt_e4m3x2(value(bf16_lo(w0)), value(bf16_hi(w0))) |
+               (cvt_e4m3x2(value(bf16_lo(w1)), value(bf16_hi(w1))) << 16);
+    }
+};
+
+// Pass 2: every workgroup folds the partial maxima (or reads the static
+// scale), then quantizes its band of rows.
+__global__ __launch_bounds__(256) void tensor_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                           int64_t rows, int64_t k, int64_t rows_per_block,
+                                                           const float* __restrict__ partial, int nparts,
+                                                           const float* __restrict__ static_scale,
+                                                           uint8_t* __restrict__ q, int64_t ldq,
+                                                           float* __restrict__ scale_out) {
+    __shared__ float red[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    TensorQuant tq;
+    if (static_scale) {
+        tq.s = *static_scale;
+        tq.exact_div = true;
+    } else {
+        float a = 0.0f;
+        for (int i = threadIdx.x; i < nparts; i += 256) a = fmaxf(a, partial[i]);
+        a = wave_max(a);
+        if (lane == 0) red[wave] = a;
+        __syncthreads();
+        a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        tq.s = row_scale(a, kE4M3Max);
+        tq.exact_div = false;
+    }
+    tq.r = 1.0f / tq.s;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = tq.s;
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+    const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
+    const bool vec = (k % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && ((uintptr_t)x % 16 == 0) &&
+                     ((uintptr_t)q % 8 == 0);
+    for (int64_t r = r0 + wave; r < r1; r += 4) {
+        const uint16_t* xr = x + r * ldx;
+        uint8_t* qr = q + r * ldq;
+        if (vec) {
+            const uint4* xv = reinterpret_cast<const uint4*>(xr);
+            uint2* qv = reinterpret_cast<uint2*>(qr);
+            for (int64_t j = lane; j < (k >> 3); j += 64) {
+                uint4 v = xv[j];
+                uint2 o;
+                o.x = tq.pack4(v.x, v.y);
+                o.y = tq.pack4(v.z, v.w);
+                qv[j] = o;
+            }
+        } else {
+            for (int64_t j = lane; j < k; j += 64) qr[j] = (uint8_t)(tq.pack4(xr[j], 0u) & 0xFFu);
+        }
+    }
+}
+
+int64_t tensor_quant_parts(int64_t rows, int64_t k) {
+    // Enough bands to fill the chip for the amax pass, few enough that every
+    // workgroup of the second pass folds them quickly.
+    const int64_t elems = rows * k;
+    int64_t parts = (elems + 65535) / 65536;
+    if (parts > 1024) parts = 1024;
+    if (parts > rows) parts = rows;
+    return parts < 1 ? 1 : parts;
+}
+
+hipError_t launch_quant_tensor_e4m3(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k,
+                                    const float* static_scale, float* partial, uint8_t* q, int64_t ldq,
+                                    float* scale_out, hipStream_t st) {
+    const int64_t parts = tensor_quant_parts(rows, k);
+    const int64_t rpb = (rows + parts - 1) / parts;
+    const int64_t blocks = (rows + rpb - 1) / rpb;
+    if (!static_scale) {
+        hipLaunchKernelGGL(tensor_amax_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, ldx, rows, k, rpb,
+                           partial);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(tensor_quant_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, ldx, rows, k, rpb,
+                       (const float*)partial, (int)blocks, static_scale, q, ldq, scale_out);
+    return hipGetLastError();
+}
+
+}  // namespace h3q

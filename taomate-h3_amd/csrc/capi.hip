@@ -1,0 +1,195 @@
+// C ABI entry points (include/taomate_h3_amd.h): host-side argument checks,
+// then one or two kernel launches on the caller's stream.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/taomate_h3_amd.h"
+#include "h3q_kernels.hpp"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_error, sizeof g_error, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok() {
+    g_error[0] = '\0';
+    return H3Q_OK;
+}
+
+int check_launch(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(H3Q_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+__attribute__((visibility("default"))) int h3q_version(void) { return 100; }
+
+__attribute__((visibility("default"))) const char* h3q_last_error(void) { return g_error; }
+
+__attribute__((visibility("default"))) int h3q_quant_rows(const void* x, int64_t rows, int64_t cols, int64_t ldx,
+                                                          int format, int rounding, void* codes, int64_t ldq,
+                                                          float* scales, void* stream) {
+    if (rows < 0 || cols < 0) return fail(H3Q_ERR_INVALID, "h3q_quant_rows: negative shape [%lld, %lld]",
+                                          (long long)rows, (long long)cols);
+    if (format != H3Q_FMT_E4M3FN && format != H3Q_FMT_INT8)
+        return fail(H3Q_ERR_INVALID, "h3q_quant_rows: unknown format %d", format);
+    if (rounding != H3Q_ROUND_DIV && rounding != H3Q_ROUND_RCP_MUL)
+        return fail(H3Q_ERR_INVALID, "h3q_quant_rows: unknown rounding %d", rounding);
+    if (format == H3Q_FMT_E4M3FN && rounding != H3Q_ROUND_DIV)
+        return fail(H3Q_ERR_UNSUPPORTED, "h3q_quant_rows: e4m3fn codes use the division form only");
+    if (ldx < cols || ldq < cols) return fail(H3Q_ERR_INVALID, "h3q_quant_rows: leading dimension below cols");
+    if (rows == 0) return ok();
+    if (!x || !codes || !scales) return fail(H3Q_ERR_INVALID, "h3q_quant_rows: null pointer");
+    if (cols == 0) return fail(H3Q_ERR_INVALID, "h3q_quant_rows: zero-width rows have no scale");
+    return check_launch(h3q::launch_quant_rows((const uint16_t*)x, ldx, rows, cols, format, rounding,
+                                               (uint8_t*)codes, ldq, scales, (hipStream_t)stream),
+                        "h3q_quant_rows");
+}
+
+__attribute__((visibility("default"))) int64_t h3q_quant_tensor_workspace_floats(int64_t rows, int64_t cols) {
+    if (rows <= 0 || cols <= 0) return 1;
+    return h3q::tensor_quant_parts(rows, cols);
+}
+
+__attribute__((visibility("default"))) int h3q_quant_tensor_e4m3(const void* x, int64_t rows, int64_t cols,
+                                                                 int64_t ldx, const float* static_scale,
+                                                                 float* partial, void* codes, int64_t ldq,
+                                                                 float* scale_out, void* stream) {
+    if (rows <= 0 || cols <= 0)
+        return fail(H3Q_ERR_INVALID, "h3q_quant_tensor_e4m3: empty tensor has no amax");
+    if (ldx < cols || ldq < cols)
+        return fail(H3Q_ERR_INVALID, "h3q_quant_tensor_e4m3: leading dimension below cols");
+    if (!x || !codes || !scale_out || (!static_scale && !partial))
+        return fail(H3Q_ERR_INVALID, "h3q_quant_tensor_e4m3: null pointer");
+    return check_launch(h3q::launch_quant_tensor_e4m3((const uint16_t*)x, ldx, rows, cols, static_scale, partial,
+                                                      (uint8_t*)codes, ldq, scale_out, (hipStream_t)stream),
+                        "h3q_quant_tensor_e4m3");
+}
+
+static int check_gemm_operands(const char* who, const void* a, int64_t lda, const void* b, int64_t ldb, int64_t m,
+                               int64_t n, int64_t k, int64_t elem) {
+    if (m < 0 || n < 0 || k < 0) return fail(H3Q_ERR_INVALID, "%s: negative shape", who);
+    if (k % 16) return fail(H3Q_ERR_INVALID, "%s: k=%lld must be a multiple of 16", who, (long long)k);
+    if (lda < k * elem || ldb < k * elem) return fail(H3Q_ERR_INVALID, "%s: leading dimension below k", who);
+    if (lda % 16 || ldb % 16) return fail(H3Q_ERR_INVALID, "%s: lda/ldb must be multiples of 16 bytes", who);
+    if (!aligned(a, 16) || !aligned(b, 16)) return fail(H3Q_ERR_INVALID, "%s: a/b must be 16-byte aligned", who);
+    // Block-relative buffer offsets are 32-bit: 256 rows of the larger stride must stay below 2^31.
+    if (lda >= (int64_t(1) << 23) || ldb >= (int64_t(1) << 23))
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: row stride above 8 MiB", who);
+    if ((m + 255) / 256 * ((n + 255) / 256) >= (int64_t(1) << 31))
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: too many output tiles", who);
+    return H3Q_OK;
+}
+
+__attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void* a, int64_t lda,
+                                                         const float* a_scale, int a_scale_kind, const void* b,
+                                                         int64_t ldb, const float* b_scale, int b_scale_kind,
+                                                         const void* bias, const void* lora_t, int64_t ldt,
+                                                         const void* lora_b, int64_t ldlb, int64_t lora_rank,
+                                                         float lora_scale, void* out, int64_t ldo, int64_t m,
+                                                         int64_t n, int64_t k, void* stream) {
+    const char* who = "h3q_scaled_mm";
+    if (format != H3Q_FMT_E4M3FN && format != H3Q_FMT_INT8)
+        return fail(H3Q_ERR_INVALID, "%s: unknown format %d", who, format);
+    if (int rc = check_gemm_operands(who, a, lda, b, ldb, m, n, k, 1)) return rc;
+    for (int kind : {a_scale_kind, b_scale_kind})
+        if (kind != H3Q_SCALE_PER_ROW && kind != H3Q_SCALE_PER_TENSOR)
+            return fail(H3Q_ERR_INVALID, "%s: unknown scale kind %d", who, kind);
+    if (ldo < n) return fail(H3Q_ERR_INVALID, "%s: ldo below n", who);
+    if ((lora_t == nullptr) != (lora_b == nullptr))
+        return fail(H3Q_ERR_INVALID, "%s: lora_t and lora_b must be given together", who);
+    if (lora_t) {
+        if (lora_rank <= 0 || lora_rank > 128 || lora_rank % 8)
+            return fail(H3Q_ERR_UNSUPPORTED, "%s: LoRA rank %lld (fused epilogue takes 8..128, multiple of 8)",
+                        who, (long long)lora_rank);
+        if (ldt < lora_rank || ldlb < lora_rank || ldt % 8 || ldlb % 8 || !aligned(lora_t, 16) ||
+            !aligned(lora_b, 16))
+            return fail(H3Q_ERR_INVALID, "%s: LoRA operands must be 16-byte aligned rows of >= rank", who);
+    }
+    if (m == 0 || n == 0) return ok();
+    if (!a || !b || !a_scale || !b_scale || !out) return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
+    h3q::GemmArgs g{};
+    g.a = a;
+    g.b = b;
+    g.lda = lda;
+    g.ldb = ldb;
+    g.m = m;
+    g.n = n;
+    g.k = k;
+    g.a_scale = a_scale;
+    g.b_scale = b_scale;
+    g.a_scale_per_row = a_scale_kind == H3Q_SCALE_PER_ROW;
+    g.b_scale_per_col = b_scale_kind == H3Q_SCALE_PER_ROW;
+    g.bias = (const uint16_t*)bias;
+    g.lora_t = (const uint16_t*)lora_t;
+    g.lora_b = (const uint16_t*)lora_b;
+    g.ldt = ldt;
+    g.ldlb = ldlb;
+    g.lora_rank = lora_rank;
+    g.lora_scale = lora_scale;
+    g.out = out;
+    g.ldo = ldo;
+    const int kind = format == H3Q_FMT_E4M3FN ? h3q::kOpE4M3 : h3q::kOpInt8;
+    return check_launch(h3q::launch_gemm(kind, false, g, (hipStream_t)stream), who);
+}
+
+__attribute__((visibility("default"))) int h3q_gemm_i8_i32(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                                           void* out, int64_t ldo, int64_t m, int64_t n, int64_t k,
+                                                           void* stream) {
+    const char* who = "h3q_gemm_i8_i32";
+    if (int rc = check_gemm_operands(who, a, lda, b, ldb, m, n, k, 1)) return rc;
+    if (ldo < n) return fail(H3Q_ERR_INVALID, "%s: ldo below n", who);
+    if (m == 0 || n == 0) return ok();
+    if (!a || !b || !out) return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
+    h3q::GemmArgs g{};
+    g.a = a;
+    g.b = b;
+    g.lda = lda;
+    g.ldb = ldb;
+    g.m = m;
+    g.n = n;
+    g.k = k;
+    g.out = out;
+    g.ldo = ldo;
+    return check_launch(h3q::launch_gemm(h3q::kOpInt8, true, g, (hipStream_t)stream), who);
+}
+
+__attribute__((visibility("default"))) int h3q_lora_down(const void* x, int64_t ldx, const void* lora_a,
+                                                         int64_t lda, void* t, int64_t ldt, int64_t m, int64_t k,
+                                                         int64_t rank, void* stream) {
+    const char* who = "h3q_lora_down";
+    if (k % 8) return fail(H3Q_ERR_INVALID, "%s: k=%lld must be a multiple of 8", who, (long long)k);
+    if (m < 0 || k < 0 || rank <= 0) return fail(H3Q_ERR_INVALID, "%s: bad shape", who);
+    if (ldx < k || lda < k || ldt < rank) return fail(H3Q_ERR_INVALID, "%s: leading dimension too small", who);
+    if (ldx % 8 || lda % 8 || !aligned(x, 16) || !aligned(lora_a, 16))
+        return fail(H3Q_ERR_INVALID, "%s: x / lora_a rows must be 16-byte aligned", who);
+    if (ldx * 2 >= (int64_t(1) << 23) || lda * 2 >= (int64_t(1) << 23))
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: row stride above 8 MiB", who);
+    if (m == 0) return ok();
+    if (!x || !lora_a || !t) return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
+    h3q::GemmArgs g{};
+    g.a = x;
+    g.b = lora_a;
+    g.lda = ldx * 2;
+    g.ldb = lda * 2;
+    g.m = m;
+    g.n = rank;
+    g.k = k;
+    g.out = t;
+    g.ldo = ldt;
+    return check_launch(h3q::launch_gemm(h3q::kOpBF16, false, g, (hipStream_t)stream), who);
+}
+
+}  // extern "C"

@@ -1,0 +1,61 @@
+// Shared device helpers for the gfx950 (CDNA4) quantized-linear kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "quant_math.h"
+
+namespace h3q {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+#define H3Q_LDS __attribute__((address_space(3)))
+
+// Code formats (mirrored by include/taomate_h3_amd.h).
+enum Format : int { kFmtE4M3 = 0, kFmtInt8 = 1 };
+// Rounding forms of a per-row quantizer.
+enum Rounding : int { kRoundDiv = 0, kRoundRcpMul = 1 };
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// binary32 -> bf16 bits, round to nearest even (finite inputs; NaN stays NaN).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t b = __float_as_uint(f);
+    if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (b >> 16) | 0x40u;
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float round_to_bf16(float f) {
+    return __uint_as_float(f32_to_bf16_bits(f) << 16);
+}
+
+// Wavefront-wide maximum of a non-negative float (64 lanes, butterfly).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Two binary32 values (already clamped to +-448) -> two e4m3fn codes in the
+// low 16 bits.  gfx950's v_cvt_pk_fp8_f32 produces OCP e4m3fn with round to
+// nearest even; the test suite compares it with the oracle over every bf16
+// value.
+__device__ __forceinline__ uint32_t cvt_e4m3x2(float a, float b) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+}
+
+// Buffer resource over [base, base + bytes): loads at offsets >= bytes return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+}  // namespace h3q

@@ -1,0 +1,202 @@
+"""Tensor-level wrappers of the native entry points.
+
+Each function checks dtypes, devices, shapes and strides on the host, raises
+before any launch when they are wrong, and enqueues the kernels on the
+current HIP stream of the input's device.  Output tensors may be supplied
+(workspace reuse) or are allocated from torch's caching allocator.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+FMT_E4M3FN = 0
+FMT_INT8 = 1
+ROUND_DIV = 0
+ROUND_RCP_MUL = 1
+SCALE_PER_TENSOR = 0
+SCALE_PER_ROW = 1
+
+_CODE_DTYPES = {FMT_E4M3FN: torch.float8_e4m3fn, FMT_INT8: torch.int8}
+_FORMATS = {torch.float8_e4m3fn: FMT_E4M3FN, torch.int8: FMT_INT8}
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _require_gpu(name: str, *tensors: torch.Tensor | None) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(f"{name}: tensors must be on a ROCm GPU, got {t.device}")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise RuntimeError(f"{name}: tensors on different devices ({device}, {t.device})")
+    return device
+
+
+def _rows_2d(name: str, t: torch.Tensor, dtype: torch.dtype) -> None:
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
+    if t.ndim != 2 or (t.shape[1] > 1 and t.stride(1) != 1):
+        raise ValueError(f"{name}: expected a 2-D tensor with unit stride along the last dimension")
+
+
+def code_dtype(fmt: int) -> torch.dtype:
+    return _CODE_DTYPES[fmt]
+
+
+def quant_rows(x: torch.Tensor, fmt: int, rounding: int = ROUND_DIV, *, codes: torch.Tensor | None = None,
+               scales: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row quantization of bf16 ``x [rows, K]`` -> (codes [rows, K], scales [rows, 1] fp32)."""
+    _require_gpu("quant_rows", x, codes, scales)
+    _rows_2d("quant_rows x", x, torch.bfloat16)
+    rows, cols = x.shape
+    if codes is None:
+        codes = torch.empty((rows, cols), device=x.device, dtype=_CODE_DTYPES[fmt])
+    if scales is None:
+        scales = torch.empty((rows, 1), device=x.device, dtype=torch.float32)
+    _rows_2d("quant_rows codes", codes, _CODE_DTYPES[fmt])
+    if tuple(codes.shape) != (rows, cols):
+        raise ValueError(f"quant_rows: codes shape {tuple(codes.shape)} != {(rows, cols)}")
+    if scales.dtype != torch.float32 or scales.numel() != rows or not scales.is_contiguous():
+        raise ValueError("quant_rows: scales must be a contiguous fp32 tensor with one entry per row")
+    _lib.call("h3q_quant_rows", _ptr(x), rows, cols, x.stride(0) if rows else cols, fmt, rounding, _ptr(codes),
+              codes.stride(0) if rows else cols, _ptr(scales), _stream(x))
+    return codes, scales
+
+
+def quant_tensor_e4m3(x: torch.Tensor, static_scale: torch.Tensor | None = None, *,
+                      codes: torch.Tensor | None = None, scale: torch.Tensor | None = None,
+                      workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-tensor e4m3fn with the bf16 intermediate; returns (codes, 0-dim fp32 scale)."""
+    _require_gpu("quant_tensor_e4m3", x, static_scale, codes, scale, workspace)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"quant_tensor_e4m3: expected bfloat16 input, got {x.dtype}")
+    shape = tuple(x.shape)
+    x2 = x.reshape(-1, shape[-1]) if x.ndim != 2 else x
+    if x2.ndim != 2 or x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    rows, cols = x2.shape
+    if codes is None:
+        codes = torch.empty(shape, device=x.device, dtype=torch.float8_e4m3fn)
+    c2 = codes.view(rows, cols)
+    if scale is None:
+        scale = torch.empty((), device=x.device, dtype=torch.float32)
+    if static_scale is not None:
+        if static_scale.dtype != torch.float32 or static_scale.numel() != 1:
+            raise TypeError("quant_tensor_e4m3: static scale must be one fp32 value")
+        static_scale = static_scale.contiguous()
+    elif workspace is None:
+        n = int(_lib.lib().h3q_quant_tensor_workspace_floats(rows, cols))
+        workspace = torch.empty(n, device=x.device, dtype=torch.float32)
+    _lib.call("h3q_quant_tensor_e4m3", _ptr(x2), rows, cols, x2.stride(0), _ptr(static_scale), _ptr(workspace),
+              _ptr(c2), c2.stride(0), _ptr(scale), _stream(x))
+    return codes, scale
+
+
+def _scale_kind(name: str, s: torch.Tensor, count: int) -> int:
+    if s.dtype != torch.float32:
+        raise TypeError(f"{name}: scales must be fp32, got {s.dtype}")
+    if not s.is_contiguous():
+        raise ValueError(f"{name}: scales must be contiguous")
+    if s.numel() == 1 and count != 1:
+        return SCALE_PER_TENSOR
+    if s.numel() == count:
+        return SCALE_PER_ROW
+    raise ValueError(f"{name}: {s.numel()} scales for {count} rows")
+
+
+def scaled_mm(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor, b_scale: torch.Tensor, *,
+              bias: torch.Tensor | None = None, lora_t: torch.Tensor | None = None,
+              lora_b: torch.Tensor | None = None, lora_scale: float = 1.0,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 out[m, n] = a_scale[m] * (b_scale[n] * (a @ b^T)) [+ bias] [+ lora_scale * lora_t @ lora_b^T].
+
+    ``a`` [m, k] and ``b`` [n, k] are both e4m3fn or both int8 codes (``b`` in
+    the nn.Linear [out, in] layout)."""
+    _require_gpu("scaled_mm", a, b, a_scale, b_scale, bias, lora_t, lora_b, out)
+    if a.dtype not in _FORMATS or b.dtype != a.dtype:
+        raise TypeError(f"scaled_mm: operands must both be e4m3fn or int8, got {a.dtype} and {b.dtype}")
+    _rows_2d("scaled_mm a", a, a.dtype)
+    _rows_2d("scaled_mm b", b, b.dtype)
+    m, k = a.shape
+    n = b.shape[0]
+    if b.shape[1] != k:
+        raise ValueError(f"scaled_mm: inner dimensions differ ({k} vs {b.shape[1]})")
+    ak = _scale_kind("scaled_mm a_scale", a_scale, m)
+    bk = _scale_kind("scaled_mm b_scale", b_scale, n)
+    if bias is not None:
+        if bias.dtype != torch.bfloat16 or bias.numel() != n or not bias.is_contiguous():
+            raise ValueError("scaled_mm: bias must be a contiguous bf16 vector of length n")
+    rank = 0
+    if (lora_t is None) != (lora_b is None):
+        raise ValueError("scaled_mm: lora_t and lora_b go together")
+    if lora_t is not None:
+        _rows_2d("scaled_mm lora_t", lora_t, torch.bfloat16)
+        _rows_2d("scaled_mm lora_b", lora_b, torch.bfloat16)
+        rank = lora_t.shape[1]
+        if lora_t.shape[0] != m or tuple(lora_b.shape) != (n, rank):
+            raise ValueError("scaled_mm: LoRA shapes must be t [m, r] and B [n, r]")
+    if out is None:
+        out = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
+    _rows_2d("scaled_mm out", out, torch.bfloat16)
+    if tuple(out.shape) != (m, n):
+        raise ValueError(f"scaled_mm: out shape {tuple(out.shape)} != {(m, n)}")
+    if m == 0 or n == 0:
+        return out
+    _lib.call("h3q_scaled_mm", _FORMATS[a.dtype], _ptr(a), a.stride(0), _ptr(a_scale), ak, _ptr(b), b.stride(0),
+              _ptr(b_scale), bk, _ptr(bias), _ptr(lora_t), lora_t.stride(0) if lora_t is not None else 0,
+              _ptr(lora_b), lora_b.stride(0) if lora_b is not None else 0, rank, float(lora_scale), _ptr(out),
+              out.stride(0), m, n, k, _stream(a))
+    return out
+
+
+def gemm_i8_i32(a: torch.Tensor, b: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Exact int32 accumulators a @ b^T of int8 a [m, k], b [n, k]."""
+    _require_gpu("gemm_i8_i32", a, b, out)
+    _rows_2d("gemm_i8_i32 a", a, torch.int8)
+    _rows_2d("gemm_i8_i32 b", b, torch.int8)
+    m, k = a.shape
+    n = b.shape[0]
+    if b.shape[1] != k:
+        raise ValueError("gemm_i8_i32: inner dimensions differ")
+    if out is None:
+        out = torch.empty((m, n), device=a.device, dtype=torch.int32)
+    _rows_2d("gemm_i8_i32 out", out, torch.int32)
+    if m == 0 or n == 0:
+        return out
+    _lib.call("h3q_gemm_i8_i32", _ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(out), out.stride(0), m, n, k,
+              _stream(a))
+    return out
+
+
+def lora_down(x: torch.Tensor, lora_a: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """t = bf16(x @ lora_a^T) for bf16 x [m, k], lora_a [r, k]."""
+    _require_gpu("lora_down", x, lora_a, out)
+    _rows_2d("lora_down x", x, torch.bfloat16)
+    _rows_2d("lora_down lora_a", lora_a, torch.bfloat16)
+    m, k = x.shape
+    rank = lora_a.shape[0]
+    if lora_a.shape[1] != k:
+        raise ValueError("lora_down: inner dimensions differ")
+    if out is None:
+        out = torch.empty((m, rank), device=x.device, dtype=torch.bfloat16)
+    _rows_2d("lora_down out", out, torch.bfloat16)
+    if m == 0:
+        return out
+    _lib.call("h3q_lora_down", _ptr(x), x.stride(0), _ptr(lora_a), lora_a.stride(0), _ptr(out), out.stride(0), m,
+              k, rank, _stream(x))
+    return out

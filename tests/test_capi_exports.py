@@ -1,0 +1,55 @@
+"""The C-ABI library loads on the CPU host and exports exactly the entry
+points include/taomate_h3_amd.h declares (no compute calls: no GPU here)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "taomate_h3_amd.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(h3q_\w+)\s*\(", text, re.M))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert {"h3q_quant_rows", "h3q_quant_tensor_e4m3", "h3q_scaled_mm", "h3q_gemm_i8_i32",
+            "h3q_lora_down", "h3q_last_error", "h3q_version"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    from taomate_h3_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("library not built (run __graft_entry__.build())")
+    handle = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in _declared():
+        assert hasattr(handle, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert exported == _declared(), exported ^ _declared()
+    assert set(_lib.SIGNATURES) == _declared()
+
+
+def test_version_and_error_without_gpu():
+    from taomate_h3_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("library not built")
+    lib = _lib.lib()
+    assert lib.h3q_version() >= 100
+    # Argument errors are rejected on the host before any launch.
+    rc = lib.h3q_quant_rows(None, 4, 16, 16, 7, 0, None, 16, None, None)
+    assert rc == 1
+    assert b"unknown format" in lib.h3q_last_error()
+    rc = lib.h3q_scaled_mm(0, None, 16, None, 1, None, 16, None, 1, None, None, 0, None, 0, 0, 1.0, None, 8,
+                           4, 8, 24, None)
+    assert rc == 1 and b"multiple of 16" in lib.h3q_last_error()

