@@ -25,6 +25,15 @@ __device__ __forceinline__ float amax_from_packed(uint32_t m) {
     return __uint_as_float((hi > lo ? hi : lo) << 16);
 }
 
+// Integral-valued float -> int clamped to [lo, 127].  v_cvt_i32_f32 is used
+// directly for its defined NaN -> 0 and saturating behaviour (a C++ float to
+// int conversion of NaN or of an out-of-range value is undefined).
+__device__ __forceinline__ int sat_int(float v, int lo) {
+    int i;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(v));
+    return i < lo ? lo : (i > 127 ? 127 : i);
+}
+
 // One row element -> code, for each quantizer form.
 template <int FMT, int ROUND>
 struct RowQuant {
@@ -54,11 +63,11 @@ struct RowQuant {
             d = __builtin_amdgcn_fmed3f(d, -kE4M3Max, kE4M3Max);
             return cvt_e4m3x2(a, b) | (cvt_e4m3x2(c, d) << 16);
         }
-        const float lo = (ROUND == kRoundRcpMul) ? -128.0f : -kInt8Max;
-        int ia = (int)__builtin_amdgcn_fmed3f(a, lo, kInt8Max);
-        int ib = (int)__builtin_amdgcn_fmed3f(b, lo, kInt8Max);
-        int ic = (int)__builtin_amdgcn_fmed3f(c, lo, kInt8Max);
-        int id = (int)__builtin_amdgcn_fmed3f(d, lo, kInt8Max);
+        // Saturating convert: v_cvt_i32_f32 maps NaN to 0 and +-inf to the
+        // int32 limits, then an integer clamp (NaN -> 0, inf -> 127 / lo as
+        // in a saturating int8 convert).
+        const int lo = (ROUND == kRoundRcpMul) ? -128 : -127;
+        const int ia = sat_int(a, lo), ib = sat_int(b, lo), ic = sat_int(c, lo), id = sat_int(d, lo);
         return (uint32_t)(ia & 0xFF) | ((uint32_t)(ib & 0xFF) << 8) | ((uint32_t)(ic & 0xFF) << 16) |
                ((uint32_t)id << 24);
     }

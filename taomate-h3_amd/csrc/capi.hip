@@ -108,6 +108,8 @@ __attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void*
         if (kind != H3Q_SCALE_PER_ROW && kind != H3Q_SCALE_PER_TENSOR)
             return fail(H3Q_ERR_INVALID, "%s: unknown scale kind %d", who, kind);
     if (ldo < n) return fail(H3Q_ERR_INVALID, "%s: ldo below n", who);
+    // Block-relative output offsets are 32-bit: 256 rows of ldo 4-byte elements stay below 2^31.
+    if (ldo >= (int64_t(1) << 21)) return fail(H3Q_ERR_UNSUPPORTED, "%s: output row stride above 2^21", who);
     if ((lora_t == nullptr) != (lora_b == nullptr))
         return fail(H3Q_ERR_INVALID, "%s: lora_t and lora_b must be given together", who);
     if (lora_t) {
@@ -151,6 +153,8 @@ __attribute__((visibility("default"))) int h3q_gemm_i8_i32(const void* a, int64_
     const char* who = "h3q_gemm_i8_i32";
     if (int rc = check_gemm_operands(who, a, lda, b, ldb, m, n, k, 1)) return rc;
     if (ldo < n) return fail(H3Q_ERR_INVALID, "%s: ldo below n", who);
+    // Block-relative output offsets are 32-bit: 256 rows of ldo 4-byte elements stay below 2^31.
+    if (ldo >= (int64_t(1) << 21)) return fail(H3Q_ERR_UNSUPPORTED, "%s: output row stride above 2^21", who);
     if (m == 0 || n == 0) return ok();
     if (!a || !b || !out) return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
     h3q::GemmArgs g{};
@@ -173,6 +177,7 @@ __attribute__((visibility("default"))) int h3q_lora_down(const void* x, int64_t 
     if (k % 8) return fail(H3Q_ERR_INVALID, "%s: k=%lld must be a multiple of 8", who, (long long)k);
     if (m < 0 || k < 0 || rank <= 0) return fail(H3Q_ERR_INVALID, "%s: bad shape", who);
     if (ldx < k || lda < k || ldt < rank) return fail(H3Q_ERR_INVALID, "%s: leading dimension too small", who);
+    if (ldt >= (int64_t(1) << 21)) return fail(H3Q_ERR_UNSUPPORTED, "%s: output row stride above 2^21", who);
     if (ldx % 8 || lda % 8 || !aligned(x, 16) || !aligned(lora_a, 16))
         return fail(H3Q_ERR_INVALID, "%s: x / lora_a rows must be 16-byte aligned", who);
     if (ldx * 2 >= (int64_t(1) << 23) || lda * 2 >= (int64_t(1) << 23))

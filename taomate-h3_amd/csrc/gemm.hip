@@ -3,18 +3,28 @@
 //   out[m, n] = epilogue( sum_k A[m, k] * B[n, k] )
 //
 // A and B are both K-contiguous ("TN": activations [M, K] and nn.Linear
-// weights [N, K]).  Block tile BM x BN, four wavefronts in a 2 x 2 grid, each
-// owning a (BM/2) x (BN/2) accumulator block of 32 x 32 MFMA tiles:
+// weights [N, K]).  A block tile BM x BN is split over WAVES_M x WAVES_N
+// wavefronts, each owning a (BM/WAVES_M) x (BN/WAVES_N) accumulator block of
+// 32 x 32 MFMA tiles:
 //   e4m3  v_mfma_f32_32x32x64_f8f6f4   (32 code bytes per lane per operand)
 //   int8  v_mfma_i32_32x32x32_i8       (16 bytes per lane)
 //   bf16  v_mfma_f32_32x32x16_bf16     (16 bytes per lane)
-// K advances in 128-byte tiles.  Each operand tile (rows x 128 B) is copied
-// HBM -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging) into one of two
-// LDS stages, while the MFMAs consume the other stage.  Inside a stage a row
-// is 8 chunks of 16 B stored at chunk ^ (row & 7), so the 8 lanes that share
-// a ds_read_b128 phase hit 8 distinct bank groups.  Rows beyond M / N and
-// k-chunks beyond K are fetched with an out-of-range buffer offset, which the
-// hardware returns as zeros: tails need no special path.
+//
+// Pipeline.  K advances in tiles of BK bytes.  Each operand tile (rows x BK)
+// is copied HBM -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging) into
+// a ring of STAGES LDS buffers; STAGES - 1 tiles are in flight while the
+// MFMAs consume the oldest.  One workgroup barrier per k-tile both publishes
+// the tile that just landed and frees the buffer the next copy overwrites.
+//
+// LDS layout.  A row of a stage holds BK / 16 chunks of 16 bytes; logical
+// chunk c of row r sits at physical chunk c ^ f(r), f(r) = (r / (128 / BK))
+// mod (BK / 16), so the lanes of one ds_read_b128 phase (consecutive rows,
+// same logical chunk) spread over distinct bank groups.  One wave copy
+// instruction fills 1 KiB: lane L lands at byte 16 L of it, so it fetches the
+// logical chunk that the layout assigns to that position.
+//
+// Tails.  Rows beyond M / N and chunks beyond K are fetched with an
+// out-of-range buffer offset, which the hardware returns as zeros.
 //
 // Epilogue (per 32 x 32 tile, in registers):
 //   e4m3 / int8: v = s_a[m] * (s_w[n] * float(acc)) [fma(s_a, ., bias[n])]
@@ -26,8 +36,6 @@
 #include "h3q_kernels.hpp"
 
 namespace h3q {
-
-constexpr int kBK = 128;  // bytes of K per LDS tile
 
 template <int OP>
 struct Mfma;
@@ -63,31 +71,95 @@ struct Mfma<kOpBF16> {
     }
 };
 
-// Copy rows [0, ROWS) x bytes [k0, k0 + 128) of an operand into an LDS stage.
-// One wave instruction fills 1 KiB = 8 rows; lane L lands at byte L * 16 of
-// that KiB, i.e. row L / 8, physical chunk L % 8, so it fetches logical chunk
-// (L % 8) ^ (L / 8).
-template <int ROWS>
-__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rsrc, H3Q_LDS uint8_t* dst, uint32_t ld,
+// OCC_ = waves per SIMD the register budget is sized for (1: one 4-wave
+// workgroup per CU with 512 registers per lane; 2: two workgroups per CU or
+// one 8-wave workgroup).
+template <int BM_, int BN_, int BK_, int STAGES_, int WAVES_M_, int WAVES_N_, int OCC_ = 1>
+struct Tile {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, STAGES = STAGES_, OCC = OCC_;
+    static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, NWAVES = WAVES_M * WAVES_N;
+    static constexpr int NT = 64 * NWAVES;
+    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, TM = WM / 32, TN = WN / 32;
+    static constexpr int CH = BK / 16;           // 16-byte chunks per row
+    static constexpr int ROWS_PER_KB = 1024 / BK;
+    static constexpr int STAGE_BYTES = (BM + BN) * BK;
+    static constexpr int LOADS_A = BM * BK / 1024 / NWAVES;  // copy instructions per wave per stage
+    static constexpr int LOADS_B = BN * BK / 1024 / NWAVES;
+    static constexpr int LOADS = LOADS_A + LOADS_B;
+    static_assert(BK == 64 || BK == 128, "BK");
+    static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile");
+    static_assert((BM * BK / 1024) % NWAVES == 0 && (BN * BK / 1024) % NWAVES == 0, "copy split");
+    static_assert(STAGES >= 2 && STAGES * STAGE_BYTES * (OCC * 4 / NWAVES > 0 ? OCC * 4 / NWAVES : 1) <= 160 * 1024, "LDS");
+    static_assert(LOADS * (STAGES - 2) < 64, "vmcnt");
+    // Physical chunk = logical chunk ^ swz(row).  gfx950's LDS serves 256
+    // bytes per clock, i.e. 16 lanes of a ds_read_b128 at once; those 16
+    // lanes read 16 consecutive rows at the same logical chunk, covering
+    // 16 * BK bytes, so their 16-byte slots (row * BK + 16 * phys) mod 256
+    // must all differ.  For BK = 128 rows pair up in a 256-byte window and
+    // the eight rows of equal parity need distinct chunks: swz = (r ^ r>>3)
+    // mod 8.  For BK = 64 four rows share a window and rows r, r+4, r+8, r+12
+    // need distinct chunks: swz = (r>>1 ^ r>>3) mod 2 + 2 ((r>>2) mod 2).  Both
+    // also keep any 8 consecutive rows conflict-free.
+    static __device__ __forceinline__ int swz(int r) {
+        if constexpr (BK == 128) return (r ^ (r >> 3)) & 7;
+        return (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2);
+    }
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Buffer descriptor of an operand region (4 SGPRs): base, stride 0, size in
+// bytes (offsets at or beyond it read as zero), raw-buffer format word.
+struct CopySrc {
+    v4i d;
+    __device__ __forceinline__ CopySrc(const void* base, uint32_t bytes) {
+        const uint64_t b = (uint64_t)base;
+        d = v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)b),
+                __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32) & 0xFFFF),
+                __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+    }
+};
+
+// One wave-wide 16-byte-per-lane copy global -> LDS (buffer_load_dwordx4 ...
+// lds): lane L's 16 bytes at src + voff land at LDS byte lds_base + 16 L.
+// Issued as inline asm so the compiler's wait-count pass, which cannot tell
+// that the ring buffer being filled differs from the one being read, does not
+// insert a vmcnt(0) before every LDS read; the kernel waits for its copies
+// explicitly (wait_vmcnt + ring_barrier).  M0 carries the LDS base; nothing
+// else in these kernels uses M0.
+__device__ __forceinline__ void copy16(const CopySrc& src, uint32_t lds_base, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(src.d)
+                 : "memory");
+}
+
+// Copy rows [0, ROWS) x bytes [k0, k0 + BK) of an operand into an LDS stage.
+template <class T, int ROWS>
+__device__ __forceinline__ void load_tile(const CopySrc& rsrc, H3Q_LDS uint8_t* dst, uint32_t ld,
                                           int64_t k0, int64_t kbytes, int wave, int lane) {
-    const int sub = lane >> 3;
-    const int lch = (lane & 7) ^ sub;
-    const int64_t kb = k0 + lch * 16;
-    // A k-chunk past K gets an offset above every in-range one (row * ld < 2^31).
-    const uint32_t koff = kb < kbytes ? (uint32_t)kb : 0x80000000u;
+    const int sub = lane / T::CH;  // row inside the 1 KiB copy
 #pragma unroll
-    for (int i = 0; i < ROWS / 32; ++i) {
-        const int c = wave + 4 * i;
-        const uint32_t off = (uint32_t)(c * 8 + sub) * ld + koff;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (H3Q_LDS void*)(dst + c * 1024), 16, off, 0, 0, 0);
+    for (int i = 0; i < ROWS * T::BK / 1024 / T::NWAVES; ++i) {
+        const int c = wave + T::NWAVES * i;
+        const int row = c * T::ROWS_PER_KB + sub;
+        const int64_t kb = k0 + ((lane % T::CH) ^ T::swz(row)) * 16;  // logical chunk this lane fetches
+        // A chunk past K gets an offset above every in-range one (row * ld < 2^31).
+        const uint32_t off = kb < kbytes ? (uint32_t)row * ld + (uint32_t)kb : 0x80000000u;
+        copy16(rsrc, (uint32_t)(uintptr_t)(dst + c * 1024), off);
     }
 }
 
-// Fragment of one 32-row MFMA operand for k-step s of a stage.
-template <int OP>
+// MFMA operand fragment of one 32-row block for k-step s of a stage.
+template <class T, int OP>
 __device__ __forceinline__ typename Mfma<OP>::frag_t read_frag(const H3Q_LDS uint8_t* tile, int row, int s, int g) {
-    const H3Q_LDS uint8_t* base = tile + row * kBK;
-    const int sw = row & 7;
+    const H3Q_LDS uint8_t* base = tile + row * T::BK;
+    const int sw = T::swz(row);
     if constexpr (OP == kOpE4M3) {
         const int c0 = s * 4 + g * 2;
         v4i lo = *(const H3Q_LDS v4i*)(base + ((c0 ^ sw) << 4));
@@ -99,22 +171,27 @@ __device__ __forceinline__ typename Mfma<OP>::frag_t read_frag(const H3Q_LDS uin
     }
 }
 
-template <int OP, int TM, int TN>
+// One stage of MFMAs.  The weight fragment is the MFMA's A operand and the
+// activation fragment its B operand, so accumulator tile acc[i][j] holds
+// out^T: lane L owns output row m = 32 i + L % 32 and, in accumulator slot v,
+// column n = 32 j + 8 (v / 4) + 4 (L / 32) + v % 4 -- four consecutive
+// columns per slot group, which the epilogue writes as one 8-byte store.
+template <class T, int OP>
 __device__ __forceinline__ void mma_stage(const H3Q_LDS uint8_t* sa, const H3Q_LDS uint8_t* sb, int wm0, int wn0,
-                                          int lane, typename Mfma<OP>::acc_t (&acc)[TM][TN]) {
-    constexpr int kSteps = kBK / Mfma<OP>::kStep;
+                                          int lane, typename Mfma<OP>::acc_t (&acc)[T::TM][T::TN]) {
+    constexpr int kSteps = T::BK / Mfma<OP>::kStep;
     const int r = lane & 31, g = lane >> 5;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
-        typename Mfma<OP>::frag_t af[TM], bfr[TN];
+        typename Mfma<OP>::frag_t af[T::TM], bfr[T::TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) af[i] = read_frag<OP>(sa, wm0 + 32 * i + r, s, g);
+        for (int i = 0; i < T::TM; ++i) af[i] = read_frag<T, OP>(sa, wm0 + 32 * i + r, s, g);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bfr[j] = read_frag<OP>(sb, wn0 + 32 * j + r, s, g);
+        for (int j = 0; j < T::TN; ++j) bfr[j] = read_frag<T, OP>(sb, wn0 + 32 * j + r, s, g);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < T::TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] = Mfma<OP>::run(af[i], bfr[j], acc[i][j]);
+            for (int j = 0; j < T::TN; ++j) acc[i][j] = Mfma<OP>::run(bfr[j], af[i], acc[i][j]);
     }
 }
 
@@ -140,30 +217,70 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
 
 enum Epi : int { kEpiScaled = 0, kEpiI32 = 1, kEpiBF16 = 2 };
 
-template <int OP, int BM, int BN, int EPI, bool LORA>
-__global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
-    constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
-    constexpr int kStage = (BM + BN) * kBK;
+// Workgroup barrier for the copy ring.  __syncthreads() would add a release
+// fence, which waits for every in-flight LDS copy (vmcnt(0)) and so drains the
+// ring; here the caller has already waited for exactly the stage it needs, and
+// only this wave's LDS reads must be complete before others overwrite a
+// buffer.  The asm memory clobber keeps LDS accesses on their side.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Wait until the oldest `pending + 1` copy stages of this wave have landed,
+// leaving `pending` younger stages in flight (only used while draining).
+template <class T>
+__device__ __forceinline__ void wait_stage(int pending) {
+    if constexpr (T::STAGES >= 4) {
+        if (pending >= 2) { wait_vmcnt<2 * T::LOADS>(); return; }
+    }
+    if constexpr (T::STAGES >= 3) {
+        if (pending >= 1) { wait_vmcnt<T::LOADS>(); return; }
+    }
+    wait_vmcnt<0>();
+}
+
+// Kernel variants.  The epilogue is fully unrolled (all accumulators live in
+// registers), so every choice inside it is a template parameter rather than a
+// branch: VEC (4 columns per store; needs ldo % 4 == 0, n % 4 == 0 and a
+// 16-byte aligned output) and BIAS.  The scalar-store variant (VEC = false)
+// takes the bias from a runtime check.
+template <class T, int OP, int EPI, bool LORA, bool VEC, bool BIAS>
+__global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
+    constexpr int BM = T::BM, BN = T::BN, BK = T::BK, S = T::STAGES, TM = T::TM, TN = T::TN;
     using acc_t = typename Mfma<OP>::acc_t;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds_stage0[kStage];
-    __shared__ __attribute__((aligned(1024))) uint8_t lds_stage1[kStage];
-    H3Q_LDS uint8_t* const lds0 = (H3Q_LDS uint8_t*)lds_stage0;
-    H3Q_LDS uint8_t* const lds1 = (H3Q_LDS uint8_t*)lds_stage1;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_ring[S * T::STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) float lds_sw[BN];     // this block's per-column weight scales
+    __shared__ __attribute__((aligned(16))) uint16_t lds_bias[BN];  // and bias (bf16 bits)
+    H3Q_LDS uint8_t* const lds = (H3Q_LDS uint8_t*)lds_ring;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 5, c32 = lane & 31;
     int tm, tn;
     tile_coords(tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+    const int wm0 = (wave / T::WAVES_N) * T::WM, wn0 = (wave % T::WAVES_N) * T::WN;
 
     const int64_t kbytes = (OP == kOpBF16) ? p.k * 2 : p.k;
     const int64_t rows_a = (p.m - m0) < BM ? (p.m - m0) : BM;
     const int64_t rows_b = (p.n - n0) < BN ? (p.n - n0) : BN;
-    const __amdgpu_buffer_rsrc_t ra =
-        make_rsrc((const uint8_t*)p.a + m0 * p.lda, (uint32_t)(rows_a * p.lda));
-    const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc((const uint8_t*)p.b + n0 * p.ldb, (uint32_t)(rows_b * p.ldb));
+    const CopySrc ra((const uint8_t*)p.a + m0 * p.lda, (uint32_t)(rows_a * p.lda));
+    const CopySrc rb((const uint8_t*)p.b + n0 * p.ldb, (uint32_t)(rows_b * p.ldb));
+
+    // Scales are fetched before the main loop so their latency hides behind
+    // it: each lane's row scales in registers, the block's column scales and
+    // bias in LDS (published by the first ring barrier).
+    float sa_reg[TM];
+    if constexpr (EPI == kEpiScaled) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int64_t m = m0 + wm0 + 32 * i + c32;
+            sa_reg[i] = m < p.m ? p.a_scale[p.a_scale_per_row ? m : 0] : 0.0f;
+        }
+        for (int c = threadIdx.x; c < BN; c += T::NT) {
+            const int64_t n = n0 + c;
+            lds_sw[c] = n < p.n ? p.b_scale[p.b_scale_per_col ? n : 0] : 0.0f;
+            if (BIAS || !VEC) lds_bias[c] = (p.bias && n < p.n) ? p.bias[n] : (uint16_t)0;
+        }
+    }
 
     acc_t acc[TM][TN];
 #pragma unroll
@@ -171,87 +288,128 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p, int tiles_m, i
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = acc_t{};
 
-    const int64_t ktiles = (kbytes + kBK - 1) / kBK;
-    load_tile<BM>(ra, lds0, (uint32_t)p.lda, 0, kbytes, wave, lane);
-    load_tile<BN>(rb, lds0 + BM * kBK, (uint32_t)p.ldb, 0, kbytes, wave, lane);
-    wait_vmcnt0();
-    __syncthreads();
-    for (int64_t kt = 0; kt < ktiles; ++kt) {
-        H3Q_LDS uint8_t* cur = (kt & 1) ? lds1 : lds0;
-        H3Q_LDS uint8_t* nxt = (kt & 1) ? lds0 : lds1;
-        if (kt + 1 < ktiles) {
-            load_tile<BM>(ra, nxt, (uint32_t)p.lda, (kt + 1) * kBK, kbytes, wave, lane);
-            load_tile<BN>(rb, nxt + BM * kBK, (uint32_t)p.ldb, (kt + 1) * kBK, kbytes, wave, lane);
-        }
-        mma_stage<OP, TM, TN>(cur, cur + BM * kBK, wm0, wn0, lane, acc);
-        wait_vmcnt0();
-        __syncthreads();
+    // Main loop.  The steady state always has S - 2 younger stages in flight
+    // behind the one it waits for, so its body is branch-free; the last
+    // S - 1 k-tiles drain the ring.
+    const int ktiles = (int)((kbytes + BK - 1) / BK);
+    auto issue = [&](int kt, int buf) {
+        H3Q_LDS uint8_t* dst = lds + buf * T::STAGE_BYTES;
+        load_tile<T, BM>(ra, dst, (uint32_t)p.lda, (int64_t)kt * BK, kbytes, wave, lane);
+        load_tile<T, BN>(rb, dst + BM * BK, (uint32_t)p.ldb, (int64_t)kt * BK, kbytes, wave, lane);
+    };
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s)
+        if (s < ktiles) issue(s, s);
+    int rd = 0, wr = S - 1, kt = 0;
+    for (; kt + S - 1 < ktiles; ++kt) {
+        wait_vmcnt<(S - 2) * T::LOADS>();
+        ring_barrier();
+        issue(kt + S - 1, wr);
+        const H3Q_LDS uint8_t* cur = lds + rd * T::STAGE_BYTES;
+        mma_stage<T, OP>(cur, cur + BM * BK, wm0, wn0, lane, acc);
+        rd = rd + 1 == S ? 0 : rd + 1;
+        wr = wr + 1 == S ? 0 : wr + 1;
+    }
+    for (; kt < ktiles; ++kt) {
+        wait_stage<T>(ktiles - 1 - kt);
+        ring_barrier();
+        const H3Q_LDS uint8_t* cur = lds + rd * T::STAGE_BYTES;
+        mma_stage<T, OP>(cur, cur + BM * BK, wm0, wn0, lane, acc);
+        rd = rd + 1 == S ? 0 : rd + 1;
     }
 
-    // LoRA slab: t [BM, r] and lora_b [BN, r] (bf16, r <= 128) staged into the
-    // two LDS stages, 64 rank elements (128 B) per stage.
+    // LoRA slab: t [BM, r] and lora_b [BN, r] (bf16, r <= 128 -> 256 bytes per
+    // row) staged into the first 256 / BK ring buffers.
+    constexpr int kLoraTiles = 256 / BK;
     if constexpr (LORA) {
+        static_assert(kLoraTiles <= S, "LoRA slab needs 256 bytes of K per row across the ring");
+        __syncthreads();
         const int64_t rbytes = p.lora_rank * 2;
-        const __amdgpu_buffer_rsrc_t rt =
-            make_rsrc((const uint8_t*)p.lora_t + m0 * p.ldt * 2, (uint32_t)(rows_a * p.ldt * 2));
-        const __amdgpu_buffer_rsrc_t rl =
-            make_rsrc((const uint8_t*)p.lora_b + n0 * p.ldlb * 2, (uint32_t)(rows_b * p.ldlb * 2));
-        load_tile<BM>(rt, lds0, (uint32_t)(p.ldt * 2), 0, rbytes, wave, lane);
-        load_tile<BN>(rl, lds0 + BM * kBK, (uint32_t)(p.ldlb * 2), 0, rbytes, wave, lane);
-        load_tile<BM>(rt, lds1, (uint32_t)(p.ldt * 2), kBK, rbytes, wave, lane);
-        load_tile<BN>(rl, lds1 + BM * kBK, (uint32_t)(p.ldlb * 2), kBK, rbytes, wave, lane);
-        wait_vmcnt0();
+        const CopySrc rt((const uint8_t*)p.lora_t + m0 * p.ldt * 2, (uint32_t)(rows_a * p.ldt * 2));
+        const CopySrc rl((const uint8_t*)p.lora_b + n0 * p.ldlb * 2, (uint32_t)(rows_b * p.ldlb * 2));
+#pragma unroll
+        for (int t = 0; t < kLoraTiles; ++t) {
+            H3Q_LDS uint8_t* dst = lds + t * T::STAGE_BYTES;
+            load_tile<T, BM>(rt, dst, (uint32_t)(p.ldt * 2), t * BK, rbytes, wave, lane);
+            load_tile<T, BN>(rl, dst + BM * BK, (uint32_t)(p.ldlb * 2), t * BK, rbytes, wave, lane);
+        }
+        wait_vmcnt<0>();
         __syncthreads();
     }
 
-    const int g = lane >> 5, c32 = lane & 31;
+    // Epilogue.  Stores go through a buffer resource over this block's output
+    // rows, so rows past M fall outside it and are dropped by the hardware;
+    // a column group past N is given an out-of-range offset.
+    constexpr uint32_t kEs = EPI == kEpiI32 ? 4 : 2;
+    constexpr uint32_t kDrop = 0xFFFFFFF0u;
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc((uint8_t*)p.out + m0 * p.ldo * kEs, (uint32_t)(rows_a * p.ldo * kEs));
+    const H3Q_LDS float* sw_l = (const H3Q_LDS float*)lds_sw;
+    const H3Q_LDS uint16_t* bias_l = (const H3Q_LDS uint16_t*)lds_bias;
+    const bool has_bias = VEC ? BIAS : p.bias != nullptr;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+        const uint32_t row_off = (uint32_t)(wm0 + 32 * i + c32) * (uint32_t)p.ldo * kEs;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int64_t col = n0 + wn0 + 32 * j + c32;
-            const int64_t row_base = m0 + wm0 + 32 * i + 4 * g;
-            if constexpr (EPI == kEpiI32) {
-                int32_t* out = (int32_t*)p.out;
+            // Keep each output tile's LDS reads and MFMAs from being hoisted
+            // into earlier tiles (register pressure: all accumulators are live).
+            __builtin_amdgcn_sched_barrier(0);
+            v16f lora{};
+            if constexpr (LORA) {
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int64_t row = row_base + 8 * (v >> 2) + (v & 3);
-                    if (row < p.m && col < p.n) out[row * p.ldo + col] = acc[i][j][v];
+                for (int t = 0; t < kLoraTiles; ++t) {
+                    const H3Q_LDS uint8_t* st = lds + t * T::STAGE_BYTES;
+#pragma unroll
+                    for (int s = 0; s < BK / 32; ++s)
+                        lora = Mfma<kOpBF16>::run(read_frag<T, kOpBF16>(st + BM * BK, wn0 + 32 * j + c32, s, g),
+                                                  read_frag<T, kOpBF16>(st, wm0 + 32 * i + c32, s, g), lora);
                 }
-            } else if constexpr (EPI == kEpiBF16) {
-                uint16_t* out = (uint16_t*)p.out;
+            }
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int64_t row = row_base + 8 * (v >> 2) + (v & 3);
-                    if (row < p.m && col < p.n) out[row * p.ldo + col] = (uint16_t)f32_to_bf16_bits(acc[i][j][v]);
-                }
-            } else {
-                v16f lora{};
-                if constexpr (LORA) {
+            for (int q = 0; q < 4; ++q) {
+                const int nl = wn0 + 32 * j + 8 * q + 4 * g;  // first of this slot group's 4 columns
+                const int64_t n = n0 + nl;
+                if constexpr (EPI == kEpiI32) {
+                    v4i d = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    if constexpr (VEC) {
+                        const uint32_t off = n < p.n ? row_off + (uint32_t)n * kEs : kDrop;
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, d), ro, off, 0, 0);
+                    } else {
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
-                        lora = Mfma<kOpBF16>::run(read_frag<kOpBF16>(lds0, wm0 + 32 * i + c32, s, g),
-                                                  read_frag<kOpBF16>(lds0 + BM * kBK, wn0 + 32 * j + c32, s, g),
-                                                  lora);
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t off = n + e < p.n ? row_off + (uint32_t)(n + e) * kEs : kDrop;
+                            __builtin_amdgcn_raw_buffer_store_b32((uint32_t)d[e], ro, off, 0, 0);
+                        }
+                    }
+                } else {
+                    float y[4];
+                    if constexpr (EPI == kEpiBF16) {
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
-                        lora = Mfma<kOpBF16>::run(read_frag<kOpBF16>(lds1, wm0 + 32 * i + c32, s, g),
-                                                  read_frag<kOpBF16>(lds1 + BM * kBK, wn0 + 32 * j + c32, s, g),
-                                                  lora);
-                }
-                const bool cin = col < p.n;
-                const float sw = p.b_scale[p.b_scale_per_col ? (cin ? col : 0) : 0];
-                const float bias = (p.bias && cin) ? bf16_lo(p.bias[col]) : 0.0f;
-                uint16_t* out = (uint16_t*)p.out;
+                        for (int e = 0; e < 4; ++e) y[e] = acc[i][j][4 * q + e];
+                    } else {
+                        const v4f sw4 = *(const H3Q_LDS v4f*)(sw_l + nl);
+                        v2u b4 = {0u, 0u};
+                        if (BIAS || !VEC) b4 = *(const H3Q_LDS v2u*)(bias_l + nl);
+                        const float bias[4] = {bf16_lo(b4[0]), bf16_hi(b4[0]), bf16_lo(b4[1]), bf16_hi(b4[1])};
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int64_t row = row_base + 8 * (v >> 2) + (v & 3);
-                    if (row < p.m && cin) {
-                        const float sa = p.a_scale[p.a_scale_per_row ? row : 0];
-                        const float t = __fmul_rn(sw, (float)acc[i][j][v]);
-                        float y = p.bias ? __builtin_fmaf(sa, t, bias) : __fmul_rn(sa, t);
-                        if constexpr (LORA) y = __builtin_fmaf(p.lora_scale, lora[v], y);
-                        out[row * p.ldo + col] = (uint16_t)f32_to_bf16_bits(y);
+                        for (int e = 0; e < 4; ++e) {
+                            const float t = __fmul_rn(sw4[e], (float)acc[i][j][4 * q + e]);
+                            float v = has_bias ? __builtin_fmaf(sa_reg[i], t, bias[e]) : __fmul_rn(sa_reg[i], t);
+                            if constexpr (LORA) v = __builtin_fmaf(p.lora_scale, lora[4 * q + e], v);
+                            y[e] = v;
+                        }
+                    }
+                    const uint32_t w0 = pack_bf16x2(y[0], y[1]), w1 = pack_bf16x2(y[2], y[3]);
+                    if constexpr (VEC) {
+                        const uint32_t off = n < p.n ? row_off + (uint32_t)n * kEs : kDrop;
+                        __builtin_amdgcn_raw_buffer_store_b64(v2u{w0, w1}, ro, off, 0, 0);
+                    } else {
+                        const uint16_t h[4] = {(uint16_t)w0, (uint16_t)(w0 >> 16), (uint16_t)w1, (uint16_t)(w1 >> 16)};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t off = n + e < p.n ? row_off + (uint32_t)(n + e) * kEs : kDrop;
+                            __builtin_amdgcn_raw_buffer_store_b16(h[e], ro, off, 0, 0);
+                        }
                     }
                 }
             }
@@ -259,26 +417,44 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs p, int tiles_m, i
     }
 }
 
-template <int OP, int BM, int BN, int EPI, bool LORA>
-static hipError_t launch(const GemmArgs& a, hipStream_t st) {
-    const int tiles_m = (int)((a.m + BM - 1) / BM), tiles_n = (int)((a.n + BN - 1) / BN);
-    hipLaunchKernelGGL((gemm_kernel<OP, BM, BN, EPI, LORA>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, st,
-                       a, tiles_m, tiles_n);
+template <class T, int OP, int EPI, bool LORA, bool VEC, bool BIAS>
+hipError_t launch_tile(const GemmArgs& a, hipStream_t st) {
+    const int tiles_m = (int)((a.m + T::BM - 1) / T::BM), tiles_n = (int)((a.n + T::BN - 1) / T::BN);
+    hipLaunchKernelGGL((gemm_kernel<T, OP, EPI, LORA, VEC, BIAS>), dim3((unsigned)(tiles_m * tiles_n)), dim3(T::NT), 0,
+                       st, a, tiles_m, tiles_n);
     return hipGetLastError();
 }
 
-hipError_t launch_gemm(int kind, bool raw_i32, const GemmArgs& a, hipStream_t st) {
+// Selects the epilogue variant for a scaled GEMM.
+template <class T, int OP, bool LORA>
+hipError_t launch_scaled(const GemmArgs& a, hipStream_t st) {
+    if (!a.out_vec) return launch_tile<T, OP, kEpiScaled, LORA, false, false>(a, st);
+    return a.bias ? launch_tile<T, OP, kEpiScaled, LORA, true, true>(a, st)
+                  : launch_tile<T, OP, kEpiScaled, LORA, true, false>(a, st);
+}
+
+// Large-GEMM configuration: 256 x 256 block, 128-byte k-tiles, 2-deep ring
+// (128 KiB of LDS), eight waves (2 x 4) of 128 x 64, two per SIMD so one
+// wave's MFMAs overlap the other's LDS reads.  Chosen by sweeping tile shape,
+// k-tile, ring depth and wave count at the BASELINE shapes on MI355X.
+using TileBig = Tile<256, 256, 128, 2, 2, 4, 2>;
+// LoRA down-projection (N = rank <= 128): 128 x 128 blocks, bf16.
+using TileLora = Tile<128, 128, 64, 4, 2, 2>;
+
+hipError_t launch_gemm(int kind, bool raw_i32, const GemmArgs& args, hipStream_t st) {
+    GemmArgs a = args;
+    a.out_vec = (a.ldo % 4 == 0) && (a.n % 4 == 0) && ((uintptr_t)a.out % 16 == 0);
     const bool lora = a.lora_t != nullptr;
-    if (kind == kOpE4M3) {
-        return lora ? launch<kOpE4M3, 256, 256, kEpiScaled, true>(a, st)
-                    : launch<kOpE4M3, 256, 256, kEpiScaled, false>(a, st);
-    }
+    if (kind == kOpE4M3)
+        return lora ? launch_scaled<TileBig, kOpE4M3, true>(a, st) : launch_scaled<TileBig, kOpE4M3, false>(a, st);
     if (kind == kOpInt8) {
-        if (raw_i32) return launch<kOpInt8, 256, 256, kEpiI32, false>(a, st);
-        return lora ? launch<kOpInt8, 256, 256, kEpiScaled, true>(a, st)
-                    : launch<kOpInt8, 256, 256, kEpiScaled, false>(a, st);
+        if (raw_i32)
+            return a.out_vec ? launch_tile<TileBig, kOpInt8, kEpiI32, false, true, false>(a, st)
+                             : launch_tile<TileBig, kOpInt8, kEpiI32, false, false, false>(a, st);
+        return lora ? launch_scaled<TileBig, kOpInt8, true>(a, st) : launch_scaled<TileBig, kOpInt8, false>(a, st);
     }
-    return launch<kOpBF16, 128, 128, kEpiBF16, false>(a, st);
+    return a.out_vec ? launch_tile<TileLora, kOpBF16, kEpiBF16, false, true, false>(a, st)
+                     : launch_tile<TileLora, kOpBF16, kEpiBF16, false, false, false>(a, st);
 }
 
 }  // namespace h3q

@@ -14,6 +14,10 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 #define H3Q_LDS __attribute__((address_space(3)))
 
@@ -30,6 +34,12 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
     uint32_t b = __float_as_uint(f);
     if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (b >> 16) | 0x40u;
     return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+// Two binary32 values -> two bf16 (round to nearest even) in one word, low
+// half first: gfx950's v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{lo, hi}, v2bf));
 }
 
 __device__ __forceinline__ float round_to_bf16(float f) {

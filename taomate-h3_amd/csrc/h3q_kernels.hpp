@@ -36,6 +36,7 @@ struct GemmArgs {
     float lora_scale;
     void* out;              // bf16 [m, n] or int32 [m, n]
     int64_t ldo;            // in elements
+    int out_vec;            // ldo % 4 == 0, n % 4 == 0 and out 16-byte aligned: 4 columns per store
 };
 
 // out = epilogue(A @ B^T).  kind: kOpE4M3 / kOpInt8 scaled to bf16 (with
