@@ -1,0 +1,301 @@
+"""Parallel linear layers and the quantized-linear dispatch.
+
+Drop-in for the quantized-linear seam of H3/distributed/linear.py:15-191 and
+FL/distributed/linear.py:16-181:
+
+* ``_module_linear(module, inputs, bias)`` (H3/distributed/linear.py:15-33)
+  dispatches on module attributes: ``_cutlass_w8a8_weight_scale`` -> int8
+  W8A8, ``_fp8_w8a8_weight_scale`` -> per-token x per-channel FP8 W8A8 (the
+  BASELINE format; no counterpart in the reference), ``_fp8_weight_scale`` ->
+  per-tensor FP8 (FL), otherwise ``F.linear``.
+* ``_linear(...)`` keeps FL's functional signature (FL/distributed/linear.py:50-101)
+  including the "cannot combine" error.
+* ``_module_fp8_input_scale`` and the two context managers keep FL's
+  calibrated-scale protocol (FL/distributed/linear.py:16-47,104-128).
+
+This build runs on one GPU: tensor parallelism is represented (the same
+constructor arguments and weight-slicing helpers) but a ``ParallelContext``
+with more than one rank raises, since the collectives that TP needs are not
+part of it.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Iterator, Sequence
+from contextlib import contextmanager
+from contextvars import ContextVar
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .. import ops
+
+
+@dataclass(frozen=True)
+class ParallelContext:
+    """Tensor-parallel placement of this rank (H3/distributed/parallel.py:9-31)."""
+
+    tp_world_size: int = 1
+    tp_rank: int = 0
+
+    def __post_init__(self) -> None:
+        if self.tp_world_size != 1 or self.tp_rank != 0:
+            raise NotImplementedError("tensor parallelism over several GPUs is not part of this single-GPU build")
+
+
+_DEFAULT_CONTEXT = ParallelContext()
+
+
+def current_parallel_context() -> ParallelContext:
+    return _DEFAULT_CONTEXT
+
+
+# ------------------------------------------------------------------ dispatch
+
+def _fp8_w8a8_linear(inputs: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                     bias: torch.Tensor | None) -> torch.Tensor:
+    """Per-token dynamic e4m3fn activations x per-channel e4m3fn weights."""
+    shape = (*inputs.shape[:-1], int(weight.shape[0]))
+    flat = inputs.reshape(-1, int(inputs.shape[-1])).contiguous()
+    q, s = ops.quant_rows(flat, ops.FMT_E4M3FN, ops.ROUND_DIV)
+    out = ops.scaled_mm(q, weight, s.reshape(-1), weight_scale.reshape(-1), bias=bias)
+    return out.reshape(shape)
+
+
+def _fp8_tensor_linear(inputs: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                       bias: torch.Tensor | None, input_scale: torch.Tensor | None) -> torch.Tensor:
+    """Per-tensor FP8 (FL/distributed/linear.py:80-101): dynamic or static
+    activation scale, then the scaled GEMM in place of torch._scaled_mm."""
+    from ..inference.fused_kernels import quantize_fp8_e4m3, quantize_fp8_e4m3_dynamic
+
+    shape = (*inputs.shape[:-1], int(weight.shape[0]))
+    flat = inputs.reshape(-1, int(inputs.shape[-1]))
+    if input_scale is None:
+        q, input_scale = quantize_fp8_e4m3_dynamic(flat)
+    else:
+        q = quantize_fp8_e4m3(flat, input_scale)
+    if bias is not None and bias.dtype != torch.bfloat16:
+        bias = bias.to(torch.bfloat16)
+    out = ops.scaled_mm(q, weight, input_scale.reshape(1).to(torch.float32),
+                        weight_scale.reshape(1).to(torch.float32), bias=bias)
+    return out.reshape(shape)
+
+
+def _module_linear(module: nn.Module, inputs: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    """H3/distributed/linear.py:15-33 plus the FP8 formats."""
+    scale = getattr(module, "_cutlass_w8a8_weight_scale", None)
+    if scale is not None:
+        from ..inference.w8a8 import cutlass_w8a8_linear
+
+        return cutlass_w8a8_linear(
+            inputs,
+            module.weight,
+            scale,
+            bias=bias,
+            workspace=getattr(module, "_cutlass_w8a8_workspace", None),
+            weight_t=getattr(module, "_cutlass_w8a8_weight_t", None),
+            weight_scale_t=getattr(module, "_cutlass_w8a8_weight_scale_t", None),
+        )
+    fp8_rows = getattr(module, "_fp8_w8a8_weight_scale", None)
+    if fp8_rows is not None:
+        return _fp8_w8a8_linear(inputs, module.weight, fp8_rows, bias)
+    fp8_tensor = getattr(module, "_fp8_weight_scale", None)
+    if fp8_tensor is not None:
+        return _fp8_tensor_linear(inputs, module.weight, fp8_tensor, bias, _module_fp8_input_scale(module, inputs))
+    return F.linear(inputs, module.weight, bias)
+
+
+def _linear(inputs: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+            fp8_weight_scale: torch.Tensor | None, fp8_input_scale: torch.Tensor | None = None,
+            cutlass_w8a8_weight_scale: torch.Tensor | None = None, cutlass_w8a8_workspace: object | None = None,
+            cutlass_w8a8_weight_t: torch.Tensor | None = None,
+            cutlass_w8a8_weight_scale_t: torch.Tensor | None = None) -> torch.Tensor:
+    """FL/distributed/linear.py:50-101."""
+    if cutlass_w8a8_weight_scale is not None:
+        if fp8_weight_scale is not None:
+            raise RuntimeError("a linear cannot combine CUTLASS W8A8 with another quantizer")
+        from ..inference.w8a8 import cutlass_w8a8_linear
+
+        return cutlass_w8a8_linear(inputs, weight, cutlass_w8a8_weight_scale, bias=bias,
+                                   workspace=cutlass_w8a8_workspace, weight_t=cutlass_w8a8_weight_t,
+                                   weight_scale_t=cutlass_w8a8_weight_scale_t)
+    if fp8_weight_scale is None:
+        return F.linear(inputs, weight, bias)
+    return _fp8_tensor_linear(inputs, weight, fp8_weight_scale, bias, fp8_input_scale)
+
+
+# ------------------------------------------------ calibrated FP8 input scale
+
+_FP8_ACTIVATION_SCALE_POLICY: ContextVar[str] = ContextVar("taomate_h3_amd_fp8_activation_scale_policy",
+                                                           default="current")
+_FP8_ACTIVATION_CALIBRATION_SUSPENDED: ContextVar[bool] = ContextVar(
+    "taomate_h3_amd_fp8_activation_calibration_suspended", default=False)
+
+
+@contextmanager
+def use_fp8_activation_scale_policy(policy: str) -> Iterator[None]:
+    """Select local-current or cross-stage-shared calibrated FP8 scales."""
+    if policy not in {"current", "prefix_shared"}:
+        raise ValueError("unsupported FP8 activation scale policy")
+    token = _FP8_ACTIVATION_SCALE_POLICY.set(policy)
+    try:
+        yield
+    finally:
+        _FP8_ACTIVATION_SCALE_POLICY.reset(token)
+
+
+@contextmanager
+def suspend_fp8_activation_calibration() -> Iterator[None]:
+    """Run FP8 with per-forward scales without consuming calibration samples."""
+    token = _FP8_ACTIVATION_CALIBRATION_SUSPENDED.set(True)
+    try:
+        yield
+    finally:
+        _FP8_ACTIVATION_CALIBRATION_SUSPENDED.reset(token)
+
+
+def _module_fp8_input_scale(module: nn.Module, inputs: torch.Tensor) -> torch.Tensor | None:
+    """FL/distributed/linear.py:104-128: None -> dynamic; during calibration the
+    observed per-tensor scale (running max kept in ``_fp8_activation_scale``);
+    afterwards the frozen scale times the margin, or the prefix-shared scale."""
+    scale = getattr(module, "_fp8_activation_scale", None)
+    if scale is None:
+        return None
+    suspended = _FP8_ACTIVATION_CALIBRATION_SUSPENDED.get()
+    remaining = int(getattr(module, "_fp8_activation_calibration_remaining", 0))
+    if remaining > 0 or suspended:
+        observed = torch.clamp(inputs.detach().abs().amax().to(torch.float32) / 448.0, min=1.0e-12)
+        if remaining > 0 and not suspended:
+            torch.maximum(scale, observed, out=scale)
+            module._fp8_activation_calibration_remaining = remaining - 1
+        return observed
+    margin = float(getattr(module, "_fp8_activation_scale_margin", 1.0))
+    if _FP8_ACTIVATION_SCALE_POLICY.get() == "prefix_shared":
+        prefix = getattr(module, "_fp8_prefix_activation_scale", None)
+        if prefix is not None:
+            return prefix * margin
+    return scale * margin
+
+
+# ------------------------------------------------------------ linear layers
+
+class ColumnParallelLinear(nn.Module):
+    """Output-column linear (H3/distributed/linear.py:36-88)."""
+
+    def __init__(self, input_size: int, output_size: int, *, bias: bool, gather_output: bool,
+                 dtype: torch.dtype, context: ParallelContext | None = None, weight_requires_grad: bool = True,
+                 device: torch.device | str | None = None) -> None:
+        super().__init__()
+        self.parallel_context = context or current_parallel_context()
+        self.input_size = int(input_size)
+        self.output_size = int(output_size)
+        self.tp_size = self.parallel_context.tp_world_size
+        self.tp_rank = self.parallel_context.tp_rank
+        self.gather_output = bool(gather_output)
+        if self.output_size % self.tp_size:
+            raise ValueError(f"column output {self.output_size} is not divisible by TP={self.tp_size}")
+        self.local_output_size = self.output_size // self.tp_size
+        self.weight = nn.Parameter(torch.empty(self.local_output_size, self.input_size, dtype=dtype, device=device),
+                                   requires_grad=weight_requires_grad)
+        self.bias = nn.Parameter(torch.empty(self.local_output_size, dtype=dtype, device=device)) if bias else None
+
+    def forward(self, inputs: torch.Tensor) -> torch.Tensor:
+        return _module_linear(self, inputs, self.bias)
+
+    def full_weight_slice(self, value: torch.Tensor) -> torch.Tensor:
+        if tuple(value.shape) != (self.output_size, self.input_size):
+            raise ValueError("full column-parallel weight shape differs")
+        return value.narrow(0, self.tp_rank * self.local_output_size, self.local_output_size).contiguous()
+
+    def full_bias_slice(self, value: torch.Tensor) -> torch.Tensor:
+        if tuple(value.shape) != (self.output_size,):
+            raise ValueError("full column-parallel bias shape differs")
+        return value.narrow(0, self.tp_rank * self.local_output_size, self.local_output_size).contiguous()
+
+
+class MergedColumnParallelLinear(ColumnParallelLinear):
+    """Column sharding applied to fused logical projections (H3/distributed/linear.py:91-137)."""
+
+    def __init__(self, input_size: int, output_sizes: Sequence[int], *, bias: bool, gather_output: bool,
+                 dtype: torch.dtype, context: ParallelContext | None = None, weight_requires_grad: bool = True,
+                 device: torch.device | str | None = None) -> None:
+        self.output_sizes = tuple(int(v) for v in output_sizes)
+        if not self.output_sizes or any(v <= 0 for v in self.output_sizes):
+            raise ValueError("merged column output sizes must be positive")
+        active = context or current_parallel_context()
+        if any(v % active.tp_world_size for v in self.output_sizes):
+            raise ValueError("every merged output must be divisible by TP")
+        super().__init__(input_size, sum(self.output_sizes), bias=bias, gather_output=gather_output, dtype=dtype,
+                         context=active, weight_requires_grad=weight_requires_grad, device=device)
+        self.local_output_sizes = tuple(v // self.tp_size for v in self.output_sizes)
+
+    def _pieces(self, value: torch.Tensor) -> torch.Tensor:
+        pieces, offset = [], 0
+        for size, local in zip(self.output_sizes, self.local_output_sizes):
+            pieces.append(value.narrow(0, offset + self.tp_rank * local, local))
+            offset += size
+        return torch.cat(pieces, dim=0).contiguous()
+
+    def full_weight_slice(self, value: torch.Tensor) -> torch.Tensor:
+        if tuple(value.shape) != (self.output_size, self.input_size):
+            raise ValueError("full merged-column weight shape differs")
+        return self._pieces(value)
+
+    def full_bias_slice(self, value: torch.Tensor) -> torch.Tensor:
+        if tuple(value.shape) != (self.output_size,):
+            raise ValueError("full merged-column bias shape differs")
+        return self._pieces(value)
+
+
+class RowParallelLinear(nn.Module):
+    """Input-row linear (H3/distributed/linear.py:140-191).  With one rank the
+    partial output is the full output and the reduction is the identity."""
+
+    def __init__(self, input_size: int, output_size: int, *, bias: bool, dtype: torch.dtype,
+                 context: ParallelContext | None = None, input_is_parallel: bool = True,
+                 weight_requires_grad: bool = True, device: torch.device | str | None = None) -> None:
+        super().__init__()
+        self.parallel_context = context or current_parallel_context()
+        self.input_size = int(input_size)
+        self.output_size = int(output_size)
+        self.tp_size = self.parallel_context.tp_world_size
+        self.tp_rank = self.parallel_context.tp_rank
+        self.input_is_parallel = bool(input_is_parallel)
+        self.inference_inplace_reduce_enabled = False
+        if self.input_size % self.tp_size:
+            raise ValueError(f"row input {self.input_size} is not divisible by TP={self.tp_size}")
+        self.local_input_size = self.input_size // self.tp_size
+        self.weight = nn.Parameter(torch.empty(self.output_size, self.local_input_size, dtype=dtype, device=device),
+                                   requires_grad=weight_requires_grad)
+        self.bias = nn.Parameter(torch.empty(self.output_size, dtype=dtype, device=device)) if bias else None
+
+    def forward_local(self, inputs: torch.Tensor) -> torch.Tensor:
+        """This rank's partial output before reduction and bias."""
+        return _module_linear(self, inputs, None)
+
+    def reduce_local_output(self, value: torch.Tensor) -> torch.Tensor:
+        return value
+
+    def forward(self, inputs: torch.Tensor) -> torch.Tensor:
+        output = self.reduce_local_output(self.forward_local(inputs))
+        if self.bias is not None:
+            output = output + self.bias
+        return output
+
+    def full_weight_slice(self, value: torch.Tensor) -> torch.Tensor:
+        if tuple(value.shape) != (self.output_size, self.input_size):
+            raise ValueError("full row-parallel weight shape differs")
+        return value.narrow(1, self.tp_rank * self.local_input_size, self.local_input_size).contiguous()
+
+
+__all__ = [
+    "ColumnParallelLinear",
+    "MergedColumnParallelLinear",
+    "ParallelContext",
+    "RowParallelLinear",
+    "current_parallel_context",
+    "suspend_fp8_activation_calibration",
+    "use_fp8_activation_scale_policy",
+]

@@ -1,0 +1,133 @@
+"""Inference LoRA side branch on a quantized base linear.
+
+Drop-in for the inference part of H3/inference/lora_checkpoint.py:172-205 and
+:261-303 (wrapper, bf16 buffer materialisation, fused row reduction).  The
+reference computes the base linear, then two bf16 ``F.linear`` calls and two
+elementwise passes over the [M, N] output:
+
+    output + F.linear(F.linear(x, A), B) * scale
+
+When the base is a W8A8 linear (int8 or per-channel FP8) and the adapter
+rank is at most 128, this wrapper instead computes t = bf16(x @ A^T) with
+``h3q_lora_down`` and lets ``h3q_scaled_mm`` add ``scale * t @ B^T`` in the
+GEMM epilogue before the single bf16 rounding of the output.  Other cases
+(a BF16 base, rank above 128) keep the reference's two-GEMM formula.
+Checkpoint loading (lora_checkpoint.py:61-150) is outside this package.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Mapping
+
+import torch
+import torch.nn.functional as F
+
+from .. import ops
+
+FUSED_MAX_RANK = 128
+
+
+class H3LoRACheckpointError(RuntimeError):
+    """Raised for adapter shapes or targets the wrapper cannot serve."""
+
+
+def _fusable(base: Any, lora_a: torch.Tensor, lora_b: torch.Tensor) -> bool:
+    quantized = (getattr(base, "_cutlass_w8a8_weight_scale", None) is not None
+                 or getattr(base, "_fp8_w8a8_weight_scale", None) is not None)
+    rank = int(lora_a.shape[0])
+    return (quantized and lora_a.dtype == torch.bfloat16 and lora_b.dtype == torch.bfloat16
+            and 0 < rank <= FUSED_MAX_RANK and rank % 8 == 0 and lora_a.is_cuda)
+
+
+def fused_quantized_lora_linear(base: Any, inputs: torch.Tensor, lora_a: torch.Tensor, lora_b: torch.Tensor,
+                                scale: float) -> torch.Tensor:
+    """base(x) + scale * (x @ A^T) @ B^T with one bf16 rounding, for a W8A8 base."""
+    shape = (*inputs.shape[:-1], int(base.weight.shape[0]))
+    flat = inputs.reshape(-1, int(inputs.shape[-1]))
+    if flat.dtype != torch.bfloat16:
+        flat = flat.to(torch.bfloat16)
+    flat = flat.contiguous()
+    t = ops.lora_down(flat, lora_a.contiguous())
+    bias = getattr(base, "bias", None)
+    if getattr(base, "_cutlass_w8a8_weight_scale", None) is not None:
+        if bias is not None:
+            raise RuntimeError("H3 W8A8 supports bias-free linears only")
+        workspace = getattr(base, "_cutlass_w8a8_workspace", None)
+        if workspace is not None:
+            q, s, out = workspace.buffers(flat, int(base.weight.shape[0]))
+        else:
+            q = s = out = None
+        q, s = ops.quant_rows(flat, ops.FMT_INT8, ops.ROUND_RCP_MUL, codes=q, scales=s)
+        w_scale = base._cutlass_w8a8_weight_scale
+    else:
+        q, s = ops.quant_rows(flat, ops.FMT_E4M3FN, ops.ROUND_DIV)
+        out = None
+        w_scale = base._fp8_w8a8_weight_scale
+    out = ops.scaled_mm(q, base.weight, s.reshape(-1), w_scale.reshape(-1), bias=bias, lora_t=t,
+                        lora_b=lora_b.contiguous(), lora_scale=float(scale), out=out)
+    return out.reshape(shape)
+
+
+class H3InferenceParallelLinearLoRA(torch.nn.Module):
+    """LoRA wrapper of a column- or row-parallel base linear
+    (H3/inference/lora_checkpoint.py:172-205).  With one rank a row-parallel
+    base needs no reduction, so both kinds share the single-rank formula."""
+
+    def __init__(self, base: Any, *, kind: str, a: torch.Tensor, b: torch.Tensor, scale: float) -> None:
+        super().__init__()
+        if kind not in ("column", "row"):
+            raise H3LoRACheckpointError(f"unknown LoRA target kind {kind}")
+        self.base = base
+        self.kind = kind
+        self.scale = float(scale)
+        self.fused_row_reduce_enabled = False
+        self._taomate_h3_inference_lora = True
+        self.register_buffer("lora_a", a, persistent=False)
+        self.register_buffer("lora_b", b, persistent=False)
+
+    def forward(self, inputs: torch.Tensor) -> torch.Tensor:
+        if _fusable(self.base, self.lora_a, self.lora_b):
+            return fused_quantized_lora_linear(self.base, inputs, self.lora_a, self.lora_b, self.scale)
+        output = self.base(inputs)
+        compute_dtype = output.dtype
+        update = F.linear(F.linear(inputs.to(compute_dtype), self.lora_a), self.lora_b)
+        if tuple(update.shape) != tuple(output.shape):
+            raise H3LoRACheckpointError("H3 inference LoRA output shape differs")
+        return output + update * self.scale
+
+
+def materialize_h3_lora_bf16_buffers_(transformer: Any) -> Mapping[str, Any]:
+    """Materialize the inference LoRA buffers once in bf16 (H3/inference/lora_checkpoint.py:261-284)."""
+    adapters = [m for m in transformer.modules() if getattr(m, "_taomate_h3_inference_lora", False)]
+    if not adapters:
+        raise H3LoRACheckpointError("BF16 LoRA buffers require a loaded adapter")
+    converted = 0
+    for module in adapters:
+        for name in ("lora_a", "lora_b"):
+            value = getattr(module, name)
+            if value.dtype != torch.bfloat16:
+                converted += int(value.numel())
+                setattr(module, name, value.to(dtype=torch.bfloat16))
+    return {"target_count": len(adapters), "buffer_count": 2 * len(adapters), "converted_numel": converted,
+            "dtype": "bfloat16"}
+
+
+def enable_h3_fused_lora_row_reduce_(transformer: Any) -> Mapping[str, Any]:
+    """Mark row-parallel adapters for the pre-reduction LoRA add (H3/inference/lora_checkpoint.py:287-303)."""
+    rows = [m for m in transformer.modules()
+            if getattr(m, "_taomate_h3_inference_lora", False) and getattr(m, "kind", None) == "row"]
+    if not rows:
+        raise H3LoRACheckpointError("fused row reduction requires a loaded adapter")
+    for module in rows:
+        module.fused_row_reduce_enabled = True
+    return {"row_parallel_module_count": len(rows), "tp_all_reduce_calls_saved_per_forward": len(rows)}
+
+
+__all__ = [
+    "FUSED_MAX_RANK",
+    "H3InferenceParallelLinearLoRA",
+    "H3LoRACheckpointError",
+    "enable_h3_fused_lora_row_reduce_",
+    "fused_quantized_lora_linear",
+    "materialize_h3_lora_bf16_buffers_",
+]

@@ -1,0 +1,276 @@
+"""The reference-interface mirror on the GPU, checked against the oracle.
+
+Covers the int8 W8A8 module path (H3/inference/w8a8.py:98-220), the FP8
+quantizers of FL/inference/fused_kernels.py:771-820, the FL linear dispatch
+(FL/distributed/linear.py:50-128 with H3/distributed/linear.py:15-33) and the
+fused LoRA wrapper (H3/inference/lora_checkpoint.py:172-205)."""
+
+from __future__ import annotations
+
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+from _util import activations, bits8, bits16, weights
+from test_gpu_gemm import _assert_fp8_close
+
+pytestmark = pytest.mark.gpu
+
+PKG = "taomate_h3_amd"
+
+
+def _mod(name):
+    return importlib.import_module(f"{PKG}.{name}")
+
+
+def _int8_reference(oracle, x, w):
+    rqa, rsa = oracle.quant_rows(bits16(x), "int8", "rcp")
+    rqw, rsw = oracle.quant_rows(bits16(w), "int8", "div")
+    return oracle.epilogue(oracle.gemm_i8_i32_fast(rqa, rqw), rsa, rsw)
+
+
+class _Block(torch.nn.Module):
+    def __init__(self, d, hidden, device):
+        super().__init__()
+        lin = _mod("distributed.linear")
+        self.attn = torch.nn.Module()
+        self.mlp = torch.nn.Module()
+        kw = dict(dtype=torch.bfloat16, device=device)
+        self.attn.qkv_proj = lin.ColumnParallelLinear(d, 3 * d, bias=False, gather_output=False, **kw)
+        self.attn.out_proj = lin.RowParallelLinear(d, d, bias=True, **kw)
+        self.mlp.fc1 = lin.ColumnParallelLinear(d, hidden, bias=False, gather_output=False, **kw)
+        self.mlp.fc2 = lin.RowParallelLinear(hidden, d, bias=True, **kw)
+
+
+class _Transformer(torch.nn.Module):
+    def __init__(self, blocks=7, d=256, hidden=512, device="cuda"):
+        super().__init__()
+        self.blocks = torch.nn.ModuleList(_Block(d, hidden, device) for _ in range(blocks))
+        gen = torch.Generator().manual_seed(4)
+        for p in self.parameters():
+            p.data.copy_((torch.randn(p.shape, generator=gen) * 0.03).to(torch.bfloat16))
+
+
+def test_quantize_weight_matches_reference_formula(oracle, device):
+    w8a8 = _mod("inference.w8a8")
+    w = weights(96, 640, seed=7)
+    q, s = w8a8._quantize_weight(w.to(device))
+    rq, rs = oracle.quant_rows(bits16(w), "int8", "div")
+    np.testing.assert_array_equal(bits8(q).view(np.int8), rq)
+    np.testing.assert_array_equal(s.cpu().numpy().ravel(), rs)
+
+
+@pytest.mark.parametrize("rows,k,limit", [(300, 512, 1024 * 1024), (300, 512, 512 * 2 * 7), (5, 256, 1)])
+def test_stream_load_chunks_equal_whole_matrix(oracle, device, rows, k, limit):
+    """Bounded row chunks (w8a8.py:98-133) give the whole-matrix codes and scales."""
+    w8a8 = _mod("inference.w8a8")
+    m = torch.nn.Module()
+    m.weight = torch.nn.Parameter(torch.empty(rows, k, dtype=torch.bfloat16, device=device))
+    m.bias = None
+    w8a8.prepare_cutlass_w8a8_stream_load_slot_(m, name="blocks.2.mlp.fc1")
+    src = weights(rows, k, seed=rows)
+    w8a8.load_cutlass_w8a8_stream_weight_(m, src, name="blocks.2.mlp.fc1", maximum_temporary_bytes=limit)
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_rows(bits16(src), "int8", "div")
+    np.testing.assert_array_equal(bits8(m.weight).view(np.int8), rq)
+    np.testing.assert_array_equal(m._cutlass_w8a8_weight_scale.cpu().numpy().ravel(), rs)
+    assert m._cutlass_w8a8_stream_loaded is True and m._cutlass_w8a8_stream_load_pending is False
+
+
+@pytest.mark.parametrize("shape", [(2, 150, 512), (1, 1, 512), (640, 512)])
+def test_cutlass_w8a8_linear_bit_exact(oracle, device, shape):
+    w8a8 = _mod("inference.w8a8")
+    k, n = shape[-1], 384
+    x = activations(int(np.prod(shape[:-1])), k, seed=3, outlier_channels=4).reshape(shape)
+    w = weights(n, k, seed=5)
+    qw, sw = w8a8._quantize_weight(w.to(device))
+    out = w8a8.cutlass_w8a8_linear(x.to(device), qw, sw, bias=None, workspace=None, weight_t=None,
+                                   weight_scale_t=None)
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (*shape[:-1], n) and out.dtype == torch.bfloat16
+    ref = _int8_reference(oracle, x.reshape(-1, k), w)
+    np.testing.assert_array_equal(bits16(out).reshape(-1, n), ref)
+
+
+def test_workspace_path_equal_and_aliased(oracle, device):
+    """The workspace path returns the same bits as the allocating path, and
+    same-width outputs on one stream share storage (w8a8.py:136-187)."""
+    w8a8 = _mod("inference.w8a8")
+    k, n = 512, 768
+    w = weights(n, k, seed=8)
+    qw, sw = w8a8._quantize_weight(w.to(device))
+    ws = w8a8.CutlassW8A8Workspace()
+    x1 = activations(200, k, seed=1, outlier_channels=3)
+    x2 = activations(120, k, seed=2, outlier_channels=3)
+    o1 = w8a8.cutlass_w8a8_linear(x1.to(device), qw, sw, bias=None, workspace=ws, weight_t=qw.t(),
+                                  weight_scale_t=sw.t())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits16(o1), _int8_reference(oracle, x1, w))
+    o2 = w8a8.cutlass_w8a8_linear(x2.to(device), qw, sw, bias=None, workspace=ws, weight_t=None,
+                                  weight_scale_t=None)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits16(o2), _int8_reference(oracle, x2, w))
+    assert o1.data_ptr() == o2.data_ptr()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        o3 = w8a8.cutlass_w8a8_linear(x2.to(device), qw, sw, bias=None, workspace=ws, weight_t=None,
+                                      weight_scale_t=None)
+    side.synchronize()
+    assert o3.data_ptr() != o2.data_ptr()
+    np.testing.assert_array_equal(bits16(o3), bits16(o2))
+
+
+def test_model_level_int8_flow(oracle, device):
+    """prepare slot -> stream load -> receipt -> workspace -> module forward,
+    on a 7-block toy DiT (the policy keeps blocks 0, 1, 4, 5, 6 in bf16)."""
+    w8a8 = _mod("inference.w8a8")
+    model = _Transformer(device=device)
+    names = w8a8.resolve_h3_cutlass_w8a8_policy(
+        [n for n, _ in model.named_modules() if n.startswith("blocks.")], policy="interior_fc1_qkv_v1")
+    assert names["quantized_linear_names"] == ["blocks.2.attn.qkv_proj", "blocks.2.mlp.fc1",
+                                               "blocks.3.attn.qkv_proj", "blocks.3.mlp.fc1"]
+    sources = {}
+    for name in names["quantized_linear_names"]:
+        module = model.get_submodule(name)
+        sources[name] = module.weight.detach().cpu().clone()
+        w8a8.prepare_cutlass_w8a8_stream_load_slot_(module, name=name)
+        w8a8.load_cutlass_w8a8_stream_weight_(module, sources[name], name=name)
+    receipt = w8a8.quantize_h3_interior_qkv_fc1_(model, policy="interior_fc1_qkv_v1")
+    assert receipt["linear_count"] == 4 and receipt["post_load_conversion_linear_count"] == 0
+    assert receipt["quantized_weight_bytes"] * 2 == receipt["source_weight_bytes"]
+    assert w8a8.enable_h3_cutlass_w8a8_workspace_(model)["linear_count"] == 4
+    x = activations(2 * 96, 256, seed=12, outlier_channels=2)
+    for name in ("blocks.2.attn.qkv_proj", "blocks.3.mlp.fc1"):
+        out = model.get_submodule(name)(x.reshape(2, 96, 256).to(device))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits16(out).reshape(192, -1), _int8_reference(oracle, x, sources[name]))
+
+
+def test_fp8_tensor_quantizers(oracle, device):
+    fk = _mod("inference.fused_kernels")
+    x = activations(333, 1040, seed=4, outlier_channels=5)
+    q, s = fk.quantize_fp8_e4m3_dynamic(x.to(device))
+    rq, rs = oracle.quant_tensor_e4m3(bits16(x))
+    np.testing.assert_array_equal(bits8(q), rq)
+    assert s.dim() == 0 and np.float32(s.item()) == rs
+    q2 = fk.quantize_fp8_e4m3(x.to(device), torch.tensor(0.0123, device=device))
+    np.testing.assert_array_equal(bits8(q2), oracle.quant_tensor_e4m3(bits16(x), np.float32(0.0123))[0])
+    q3, s3 = fk.quantize_fp8_e4m3_rowwise(x.reshape(9, 37, 1040).to(device))
+    rq3, rs3 = oracle.quant_rows(bits16(x), "e4m3")
+    assert tuple(s3.shape) == (9, 37, 1)
+    np.testing.assert_array_equal(bits8(q3).reshape(333, 1040), rq3)
+    np.testing.assert_array_equal(s3.cpu().numpy().ravel(), rs3)
+    with pytest.raises(TypeError):
+        fk.quantize_fp8_e4m3_dynamic(x.float().to(device))
+
+
+def test_fp8_w8a8_module_dispatch(oracle, device):
+    """quantize_h3_block_linears_fp8_w8a8_ + the module forward vs the exact oracle."""
+    fp8 = _mod("inference.fp8")
+    model = _Transformer(device=device)
+    originals = {n: m.weight.detach().cpu().clone() for n, m in model.named_modules()
+                 if n.endswith(("qkv_proj", "out_proj", "fc1", "fc2"))}
+    receipt = fp8.quantize_h3_block_linears_fp8_w8a8_(torch, model, policy="quality_first_residual_v1")
+    assert receipt["linear_count"] == 2 * 2  # blocks 2..3 of 7: qkv and fc1 each
+    assert model.get_submodule("blocks.3.attn.qkv_proj").weight.dtype == torch.float8_e4m3fn
+    # fc2 of block 2 stays bf16 and runs F.linear
+    fc2 = model.get_submodule("blocks.2.mlp.fc2")
+    assert fc2.weight.dtype == torch.bfloat16
+    xs = activations(150, 256, seed=7, outlier_channels=3)
+    fc1 = model.get_submodule("blocks.2.mlp.fc1")
+    out = fc1(xs.reshape(3, 50, 256).to(device))
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (3, 50, 512)
+    rqa, rsa = oracle.quant_rows(bits16(xs), "e4m3")
+    rqw, rsw = oracle.quant_rows(bits16(originals["blocks.2.mlp.fc1"]), "e4m3")
+    np.testing.assert_array_equal(bits8(fc1.weight), rqw)
+    _assert_fp8_close(oracle, bits16(out).reshape(150, 512), rqa, rsa, rqw, rsw, None)
+
+
+def test_fp8_per_tensor_module_dispatch(oracle, device):
+    """Dynamic per-tensor FP8 block linear with bias (FL/distributed/linear.py:80-101)."""
+    fp8 = _mod("inference.fp8")
+    lin = _mod("distributed.linear")
+    model = _Transformer(device=device)
+    fc2 = model.get_submodule("blocks.3.mlp.fc2")
+    bias = fc2.bias.detach().clone()
+    weight = fc2.weight.detach().cpu().clone()
+    receipt = fp8.quantize_h3_block_linears_dynamic_fp8_(torch, model)
+    assert receipt["linear_count"] == 28 and receipt["weight_scale"] == "static_per_tensor"
+    x = activations(130, 512, seed=9, outlier_channels=3)
+    rqa, rsa = oracle.quant_tensor_e4m3(bits16(x))
+    rqw, rsw = oracle.quant_tensor_e4m3(bits16(weight))
+    np.testing.assert_array_equal(bits8(fc2.weight), rqw)
+    # row-parallel: partial output without bias, bias added after the reduction
+    local = fc2.forward_local(x.to(device))
+    torch.cuda.synchronize()
+    _assert_fp8_close(oracle, bits16(local), rqa, np.array([rsa]), rqw, np.array([rsw]), None)
+    # FL's functional form: the bias is fused into the scaled GEMM
+    fused = lin._linear(x.to(device), fc2.weight, bias, fc2._fp8_weight_scale)
+    torch.cuda.synchronize()
+    _assert_fp8_close(oracle, bits16(fused), rqa, np.array([rsa]), rqw, np.array([rsw]), bits16(bias))
+
+
+def test_fp8_calibrated_scale_then_static(oracle, device):
+    """Calibration records the running max of amax/448; afterwards the frozen
+    scale x margin is the static activation scale (FL/distributed/linear.py:104-128)."""
+    fp8 = _mod("inference.fp8")
+    model = _Transformer(blocks=5, device=device)
+    fp8.quantize_h3_block_linears_calibrated_fp8_(torch, model, calibration_forwards=2, scale_margin=1.25)
+    fc1 = model.get_submodule("blocks.1.mlp.fc1")
+    xa = activations(64, 256, seed=1)
+    xb = (activations(64, 256, seed=2).float() * 3).to(torch.bfloat16)
+    fc1(xa.to(device))
+    fc1(xb.to(device))
+    torch.cuda.synchronize()
+    amax = max(float(xa.float().abs().max()), float(xb.float().abs().max()))
+    # torch evaluates tensor / 448.0 on the device as a multiply by the
+    # rounded reciprocal, so allow one binary32 ulp
+    assert np.isclose(fc1._fp8_activation_scale.item(), amax / 448.0, rtol=2.0 ** -23, atol=0)
+    assert fc1._fp8_activation_calibration_remaining == 0
+    xc = activations(64, 256, seed=3)
+    static = np.float32(fc1._fp8_activation_scale.item() * np.float32(1.25))
+    out = fc1(xc.to(device))
+    torch.cuda.synchronize()
+    rqa, _ = oracle.quant_tensor_e4m3(bits16(xc), static)
+    rqw = bits8(fc1.weight)
+    rsw = np.float32(fc1._fp8_weight_scale.item())
+    _assert_fp8_close(oracle, bits16(out), rqa, np.array([static]), rqw, np.array([rsw]), None)
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+def test_fused_lora_wrapper(oracle, device, fmt):
+    """H3InferenceParallelLinearLoRA on a W8A8 base takes the fused path; the
+    result is within a few bf16 ulps of the reference's three-rounding formula."""
+    lora = _mod("inference.lora")
+    w8a8 = _mod("inference.w8a8")
+    lin = _mod("distributed.linear")
+    k, n, m, rank = 512, 384, 200, 64
+    base = lin.ColumnParallelLinear(k, n, bias=False, gather_output=False, dtype=torch.bfloat16, device=device)
+    w = weights(n, k, seed=31)
+    if fmt == "int8":
+        qw, sw = w8a8._quantize_weight(w.to(device))
+        base.weight = torch.nn.Parameter(qw, requires_grad=False)
+        base.register_buffer("_cutlass_w8a8_weight_scale", sw, persistent=False)
+    else:
+        fp8 = _mod("inference.fp8")
+        qw, sw = fp8.quantize_weight_fp8_rows(w.to(device))
+        base.weight = torch.nn.Parameter(qw, requires_grad=False)
+        base.register_buffer("_fp8_w8a8_weight_scale", sw, persistent=False)
+    gen = torch.Generator().manual_seed(5)
+    la = (torch.randn(rank, k, generator=gen) * 0.02).to(torch.bfloat16)
+    lb = (torch.randn(n, rank, generator=gen) * 0.02).to(torch.bfloat16)
+    wrapped = lora.H3InferenceParallelLinearLoRA(base, kind="column", a=la.to(device), b=lb.to(device), scale=0.75)
+    x = activations(m, k, seed=32, outlier_channels=2)
+    out = wrapped(x.to(device))
+    base_out = base(x.to(device))
+    torch.cuda.synchronize()
+    ref = oracle.bf16_to_f32(oracle.lora_reference(bits16(x), bits16(la), bits16(lb), 0.75,
+                                                   bits16(base_out))).astype(np.float64)
+    got = oracle.bf16_to_f32(bits16(out)).astype(np.float64)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 2.0 ** -7
+    from _util import bf16_ulp
+
+    assert np.max(np.abs(got - ref)) <= 4 * np.max(bf16_ulp(ref))

@@ -1,0 +1,161 @@
+"""Host-side behaviour of the reference-interface mirror (CPU only).
+
+Policy resolution (H3/inference/w8a8.py:29-54, FL/inference/fp8.py:23-93),
+the stream-load slot protocol (H3/inference/w8a8.py:66-133), and the
+errors raised before any launch, with the reference's messages."""
+
+from __future__ import annotations
+
+import importlib
+
+import pytest
+import torch
+
+w8a8 = importlib.import_module("taomate_h3_amd.inference.w8a8")
+fp8 = importlib.import_module("taomate_h3_amd.inference.fp8")
+linear = importlib.import_module("taomate_h3_amd.distributed.linear")
+ops = importlib.import_module("taomate_h3_amd.ops")
+
+NAMES = [f"blocks.{b}.{p}" for b in range(50) for p in ("attn.qkv_proj", "attn.out_proj", "mlp.fc1", "mlp.fc2")]
+
+
+def test_int8_policy_selects_interior_qkv_and_fc1():
+    sel = w8a8.resolve_h3_cutlass_w8a8_policy(NAMES, policy="interior_fc1_qkv_v1")
+    q = sel["quantized_linear_names"]
+    assert len(q) == 90  # blocks 2..46, qkv + fc1 (SURVEY: 90 linears)
+    assert all(n.endswith((".attn.qkv_proj", ".mlp.fc1")) for n in q)
+    assert {int(n.split(".")[1]) for n in q} == set(range(2, 47))
+    assert sel["bf16_boundary_block_indices"] == [0, 1, 47, 48, 49]
+    # out_proj is not a candidate at all; fc2 and boundary qkv/fc1 stay bf16
+    assert len(sel["bf16_protected_linear_names"]) == 50 + 10
+    assert not any(n.endswith("out_proj") for n in sel["bf16_protected_linear_names"])
+
+
+def test_int8_policy_errors():
+    with pytest.raises(ValueError, match="unsupported H3 W8A8 policy"):
+        w8a8.resolve_h3_cutlass_w8a8_policy(NAMES, policy="bogus")
+    with pytest.raises(RuntimeError, match="found no DiT projections"):
+        w8a8.resolve_h3_cutlass_w8a8_policy(["proj_out"], policy="interior_fc1_qkv_v1")
+
+
+@pytest.mark.parametrize("policy,qkv_blocks,fc1", [
+    ("quality_first_residual_v1", list(range(2, 47)), 45),
+    ("interior_fc1_only_v1", [], 45),
+    ("interior_fc1_mid18_qkv_v1", list(range(16, 34)), 45),
+])
+def test_fp8_policies(policy, qkv_blocks, fc1):
+    sel = fp8.resolve_h3_dynamic_fp8_policy(NAMES, policy=policy)
+    q = sel["quantized_linear_names"]
+    assert sum(n.endswith("mlp.fc1") for n in q) == fc1
+    assert sel["quantized_qkv_block_indices"] == qkv_blocks
+    assert not any(n.endswith(("out_proj", "fc2")) for n in q)
+    assert sel["bf16_boundary_block_indices"] == [0, 1, 47, 48, 49]
+
+
+def test_fp8_policy_none_and_errors():
+    assert fp8.resolve_h3_dynamic_fp8_policy(NAMES, policy=None)["quantized_linear_names"] == NAMES
+    with pytest.raises(ValueError, match="unsupported H3 dynamic FP8 policy"):
+        fp8.resolve_h3_dynamic_fp8_policy(NAMES, policy="x")
+    with pytest.raises(ValueError, match="requires eligible linear names"):
+        fp8.resolve_h3_dynamic_fp8_policy([], policy=None)
+
+
+class _Proj(torch.nn.Module):
+    def __init__(self, n=8, k=16, bias=False, device="cpu"):
+        super().__init__()
+        self.weight = torch.nn.Parameter(torch.empty(n, k, dtype=torch.bfloat16, device=device))
+        self.bias = torch.nn.Parameter(torch.zeros(n, dtype=torch.bfloat16)) if bias else None
+
+
+def test_stream_load_slot_replaces_weight_with_int8_storage():
+    m = _Proj(device="meta")
+    w8a8.prepare_cutlass_w8a8_stream_load_slot_(m, name="blocks.3.mlp.fc1")
+    assert m.weight.dtype == torch.int8 and m.weight.requires_grad is False
+    assert tuple(m._cutlass_w8a8_weight_scale.shape) == (8, 1)
+    assert m._cutlass_w8a8_weight_scale.dtype == torch.float32
+    assert "_cutlass_w8a8_weight_scale" not in m.state_dict()
+    assert m._cutlass_w8a8_stream_load_pending is True and m._cutlass_w8a8_stream_loaded is False
+    assert m._cutlass_w8a8_source_weight_bytes == 8 * 16 * 2
+
+
+def test_stream_load_slot_errors():
+    m = _Proj()
+    m.weight.data = m.weight.data.float()
+    with pytest.raises(TypeError, match="expected an uninitialized BF16 weight"):
+        w8a8.prepare_cutlass_w8a8_stream_load_slot_(m, name="x")
+    m = _Proj()
+    m.weight.requires_grad_(False)
+    with pytest.raises(RuntimeError, match="already frozen"):
+        w8a8.prepare_cutlass_w8a8_stream_load_slot_(m, name="x")
+    with pytest.raises(RuntimeError, match="bias-free H3 projection"):
+        w8a8.prepare_cutlass_w8a8_stream_load_slot_(_Proj(bias=True), name="x")
+
+
+def test_stream_load_errors_before_any_launch():
+    m = _Proj()
+    src = torch.zeros(8, 16, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no pending CUTLASS W8A8 stream load"):
+        w8a8.load_cutlass_w8a8_stream_weight_(m, src, name="x")
+    w8a8.prepare_cutlass_w8a8_stream_load_slot_(m, name="x")
+    with pytest.raises(TypeError, match="dtype differs"):
+        w8a8.load_cutlass_w8a8_stream_weight_(m, src.float(), name="x")
+    with pytest.raises(ValueError, match="shape differs"):
+        w8a8.load_cutlass_w8a8_stream_weight_(m, src[:4], name="x")
+    with pytest.raises(ValueError, match="must be positive"):
+        w8a8.load_cutlass_w8a8_stream_weight_(m, src, name="x", maximum_temporary_bytes=0)
+
+
+def test_linear_bias_rejected_like_reference():
+    with pytest.raises(RuntimeError, match="bias-free linears only"):
+        w8a8.cutlass_w8a8_linear(torch.zeros(2, 16), torch.zeros(8, 16, dtype=torch.int8), torch.ones(8, 1),
+                                 bias=torch.zeros(8), workspace=None, weight_t=None, weight_scale_t=None)
+
+
+def test_fl_dispatch_rejects_two_quantizers():
+    with pytest.raises(RuntimeError, match="cannot combine CUTLASS W8A8"):
+        linear._linear(torch.zeros(2, 16), torch.zeros(8, 16), None, torch.ones(()), None, torch.ones(8, 1))
+
+
+def test_bf16_module_linear_is_plain_linear():
+    m = linear.ColumnParallelLinear(16, 8, bias=True, gather_output=False, dtype=torch.float32)
+    torch.nn.init.normal_(m.weight)
+    torch.nn.init.normal_(m.bias)
+    x = torch.randn(3, 16)
+    assert torch.allclose(m(x), torch.nn.functional.linear(x, m.weight, m.bias))
+
+
+def test_single_gpu_build_rejects_tensor_parallel_context():
+    with pytest.raises(NotImplementedError):
+        linear.ParallelContext(tp_world_size=2, tp_rank=0)
+
+
+def test_merged_column_weight_slice_keeps_logical_order():
+    m = linear.MergedColumnParallelLinear(4, [2, 3], bias=False, gather_output=False, dtype=torch.float32)
+    full = torch.arange(20, dtype=torch.float32).reshape(5, 4)
+    assert torch.equal(m.full_weight_slice(full), full)
+
+
+def test_ops_reject_host_tensors_before_launch():
+    x = torch.zeros(4, 16, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.quant_rows(x, ops.FMT_E4M3FN)
+    a = torch.zeros(4, 16, dtype=torch.int8)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.scaled_mm(a, a, torch.ones(4), torch.ones(4))
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ops.lora_down(x, x)
+
+
+def test_int8_stream_chunking_matches_whole_matrix_on_host_formula():
+    """The reference's claim (H3/inference/w8a8.py:105-110): row chunks with
+    per-row scales equal whole-matrix quantization -- checked on the oracle."""
+    from oracle import oracle as O
+    from _util import bits16, weights
+
+    w = weights(37, 96, seed=3)
+    whole_q, whole_s = O.quant_rows(bits16(w), "int8", "div")
+    parts = [O.quant_rows(bits16(w[i:i + 5]), "int8", "div") for i in range(0, 37, 5)]
+    import numpy as np
+
+    assert np.array_equal(np.concatenate([p[0] for p in parts]), whole_q)
+    assert np.array_equal(np.concatenate([p[1] for p in parts]), whole_s)
