@@ -34,6 +34,10 @@ extern "C" {
 #define H3Q_SCALE_PER_TENSOR 0 /* one fp32 value */
 #define H3Q_SCALE_PER_ROW 1    /* a: one per token (row of A); b: one per output channel (row of B) */
 
+/* Operand layouts of the scaled GEMM. */
+#define H3Q_LAYOUT_ROWS 0  /* row-major [rows, k] with a leading dimension */
+#define H3Q_LAYOUT_TILED 1 /* 16-row x 128-byte tiles in MFMA fragment order (see h3q_quant_rows_tiled) */
+
 /* Status codes. */
 #define H3Q_OK 0
 #define H3Q_ERR_INVALID 1     /* bad argument (checked before any launch) */
@@ -66,6 +70,31 @@ int h3q_quant_rows(const void* x, int64_t rows, int64_t cols, int64_t ldx, int f
                    void* codes, int64_t ldq, float* scales, void* stream);
 
 /*
+ * Tiled layout (H3Q_LAYOUT_TILED), the packed weight format of the GEMMs.
+ * A matrix of `rows` x `cols` codes (cols % 128 == 0) is stored as
+ * ceil(rows / 16) x (cols / 128) blocks of 2048 bytes; block (b, s) holds rows
+ * 16 b .. 16 b + 15, bytes 128 s .. 128 s + 127 at byte offset
+ * (b * cols / 128 + s) * 2048, and inside it code (r, k) sits at
+ *   (k % 32 / 16) * 1024 + (r % 16 + 16 * (k % 128 / 32)) * 16 + k % 16,
+ * i.e. the operand order of the 16 x 16 x 128 matrix instruction: each half of
+ * a lane's 32-byte fragment is one 16-byte slot, a block reads as two
+ * contiguous 1 KiB wavefront loads.  Rows past `rows` up to the next multiple
+ * of 16 may hold anything: a row of A past m only feeds output rows past m,
+ * a row of B past n only output columns past n, and those are not stored.
+ * h3q_tiled_bytes() gives the size (0 if cols % 128 != 0).
+ *
+ * h3q_quant_rows_tiled quantizes rows [row0, row0 + rows) of such a matrix,
+ * from x [rows, cols] (ldx elements), exactly as h3q_quant_rows does (same
+ * format / rounding semantics and scales, scales[i] for row row0 + i), and
+ * writes the codes into their tiled positions.  It is the offline weight
+ * quantize-and-pack step: called per row chunk it serves the 8 MiB streamed
+ * loader of H3/inference/w8a8.py:98-133 (chunks of any row count).
+ */
+int64_t h3q_tiled_bytes(int64_t rows, int64_t cols);
+int h3q_quant_rows_tiled(const void* x, int64_t rows, int64_t cols, int64_t ldx, int format, int rounding,
+                         int64_t row0, void* codes_tiled, float* scales, void* stream);
+
+/*
  * Per-tensor e4m3fn quantization with a bf16 intermediate:
  *   s = static_scale ? *static_scale : max(amax(|x|)/448, 1e-12)
  *   q = e4m3(clamp(bf16(x / s), +-448));  *scale_out = s
@@ -85,7 +114,11 @@ int h3q_quant_tensor_e4m3(const void* x, int64_t rows, int64_t cols, int64_t ldx
  *                     [+ lora_scale * sum_r lora_t[m, r] * lora_b[n, r]] )
  * a: codes [m, k] (lda bytes), b: weight codes [n, k] (ldb bytes, the
  * nn.Linear layout, i.e. cutlass_scaled_mm's B = weight.t()), format E4M3FN
- * or INT8 for both.  a_scale_kind / b_scale_kind: H3Q_SCALE_PER_ROW or
+ * or INT8 for both.  a_layout / b_layout: H3Q_LAYOUT_ROWS, or
+ * H3Q_LAYOUT_TILED (k % 128 == 0; the leading dimension is then ignored;
+ * tiled activations only for m <= 128 without LoRA).  Tiled weights are the
+ * fast format for every m (with few rows the GEMM streams them from HBM in
+ * 1 KiB loads).  a_scale_kind / b_scale_kind: H3Q_SCALE_PER_ROW or
  * H3Q_SCALE_PER_TENSOR.  bias: bf16 [n] or NULL (added as one fused
  * multiply-add: fma(a_scale, b_scale * acc, bias)).  lora_t: bf16 [m, rank]
  * (ldt elements) = x @ lora_a^T, lora_b: bf16 [n, rank] (ldlb elements), or
@@ -95,10 +128,10 @@ int h3q_quant_tensor_e4m3(const void* x, int64_t rows, int64_t cols, int64_t ldx
  * and torch._scaled_mm (FL/distributed/linear.py:92-100; FL/inference/fp8.py:135-143)
  * plus the LoRA side branch (H3/inference/lora_checkpoint.py:196-205).
  */
-int h3q_scaled_mm(int format, const void* a, int64_t lda, const float* a_scale, int a_scale_kind, const void* b,
-                  int64_t ldb, const float* b_scale, int b_scale_kind, const void* bias, const void* lora_t,
-                  int64_t ldt, const void* lora_b, int64_t ldlb, int64_t lora_rank, float lora_scale, void* out,
-                  int64_t ldo, int64_t m, int64_t n, int64_t k, void* stream);
+int h3q_scaled_mm(int format, const void* a, int64_t lda, int a_layout, const float* a_scale, int a_scale_kind,
+                  const void* b, int64_t ldb, int b_layout, const float* b_scale, int b_scale_kind, const void* bias,
+                  const void* lora_t, int64_t ldt, const void* lora_b, int64_t ldlb, int64_t lora_rank,
+                  float lora_scale, void* out, int64_t ldo, int64_t m, int64_t n, int64_t k, void* stream);
 
 /*
  * Raw int32 accumulators of the int8 GEMM: out[m, n] = sum_k a[m, k] * b[n, k]

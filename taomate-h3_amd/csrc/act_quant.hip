@@ -73,11 +73,29 @@ struct RowQuant {
     }
 };
 
+// Byte offset of code (row, k) in the output.  Row-major: row * ldq + k.
+// Tiled (the weight layout of the GEMMs, K % 128 == 0, ldq = K / 128 steps):
+// 16-row x 128-byte blocks of 2 KiB, block (row / 16, k / 128) at
+// ((row / 16) * steps + k / 128) * 2048; inside it byte k % 128 of row r lands
+// at (k % 32 / 16) * 1024 + (r % 16 + 16 * (k % 128 / 32)) * 16 + k % 16.
+// That is the operand order of v_mfma_*_16x16x128: lane l = r % 16 +
+// 16 * (k % 128 / 32) holds bytes k % 32 of its 32-byte fragment, in two
+// 16-byte halves 1 KiB apart.
+template <bool TILED>
+__device__ __forceinline__ int64_t code_offset(int64_t row, int64_t k, int64_t ldq) {
+    if constexpr (!TILED) return row * ldq + k;
+    const int64_t kk = k & 127;
+    const int64_t lane = (row & 15) + 16 * (kk >> 5);
+    return (((row >> 4) * ldq + (k >> 7)) << 11) + (((kk >> 4) & 1) << 10) + (lane << 4) + (kk & 15);
+}
+
 // Vector path: K % 8 == 0, x rows 16-byte aligned, q rows 8-byte aligned, K <= NV*512.
-template <int FMT, int ROUND, int NV>
+// TILED: codes go to the tiled layout at absolute row row0 + row.
+template <int FMT, int ROUND, int NV, bool TILED>
 __global__ __launch_bounds__(256) void quant_rows_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                              int64_t rows, int k, uint8_t* __restrict__ q,
-                                                             int64_t ldq, float* __restrict__ scales) {
+                                                             int64_t ldq, int64_t row0,
+                                                             float* __restrict__ scales) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -101,7 +119,6 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(const uint16_t* __r
     const float amax = wave_max(amax_from_packed(m));
     RowQuant<FMT, ROUND> rq;
     rq.init(amax);
-    uint2* qr = reinterpret_cast<uint2*>(q + row * ldq);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int vec = i * 64 + lane;
@@ -109,17 +126,18 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(const uint16_t* __r
             uint2 out;
             out.x = rq.pack4(v[i].x, v[i].y);
             out.y = rq.pack4(v[i].z, v[i].w);
-            qr[vec] = out;
+            *reinterpret_cast<uint2*>(q + code_offset<TILED>(row0 + row, 8 * (int64_t)vec, ldq)) = out;
         }
     }
     if (lane == 0) scales[row] = rq.s;
 }
 
 // General path (any K, any alignment): one workgroup per row, two passes.
-template <int FMT, int ROUND>
+template <int FMT, int ROUND, bool TILED>
 __global__ __launch_bounds__(256) void quant_rows_any_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                              int64_t rows, int64_t k, uint8_t* __restrict__ q,
-                                                             int64_t ldq, float* __restrict__ scales) {
+                                                             int64_t ldq, int64_t row0,
+                                                             float* __restrict__ scales) {
     __shared__ float red[4];
     const int64_t row = blockIdx.x;
     const uint16_t* xr = x + row * ldx;
@@ -133,45 +151,58 @@ __global__ __launch_bounds__(256) void quant_rows_any_kernel(const uint16_t* __r
     rq.init(amax);
     for (int64_t j = threadIdx.x; j < k; j += 256) {
         uint32_t w = xr[j];
-        q[row * ldq + j] = (uint8_t)(rq.pack4(w, 0u) & 0xFFu);
+        q[code_offset<TILED>(row0 + row, j, ldq)] = (uint8_t)(rq.pack4(w, 0u) & 0xFFu);
     }
     if (threadIdx.x == 0) scales[row] = rq.s;
 }
 
-template <int FMT, int ROUND, int NV>
+template <int FMT, int ROUND, int NV, bool TILED>
 static hipError_t launch_rows_vec(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, uint8_t* q,
-                                  int64_t ldq, float* scales, hipStream_t st) {
+                                  int64_t ldq, int64_t row0, float* scales, hipStream_t st) {
     const int64_t blocks = (rows + 3) / 4;
-    hipLaunchKernelGGL((quant_rows_vec_kernel<FMT, ROUND, NV>), dim3((unsigned)blocks), dim3(256), 0, st, x, ldx,
-                       rows, (int)k, q, ldq, scales);
+    hipLaunchKernelGGL((quant_rows_vec_kernel<FMT, ROUND, NV, TILED>), dim3((unsigned)blocks), dim3(256), 0, st, x,
+                       ldx, rows, (int)k, q, ldq, row0, scales);
     return hipGetLastError();
 }
 
-template <int FMT, int ROUND>
+template <int FMT, int ROUND, bool TILED>
 static hipError_t dispatch_rows(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, uint8_t* q, int64_t ldq,
-                                float* scales, hipStream_t st) {
-    const bool aligned = (k % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) &&
+                                int64_t row0, float* scales, hipStream_t st) {
+    const bool aligned = (k % 8 == 0) && (ldx % 8 == 0) && (TILED || ldq % 8 == 0) &&
                          ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
     const int64_t nv = (k + 511) / 512;
     if (aligned) {
-        if (nv <= 2) return launch_rows_vec<FMT, ROUND, 2>(x, ldx, rows, k, q, ldq, scales, st);
-        if (nv <= 4) return launch_rows_vec<FMT, ROUND, 4>(x, ldx, rows, k, q, ldq, scales, st);
-        if (nv <= 8) return launch_rows_vec<FMT, ROUND, 8>(x, ldx, rows, k, q, ldq, scales, st);
-        if (nv <= 12) return launch_rows_vec<FMT, ROUND, 12>(x, ldx, rows, k, q, ldq, scales, st);
-        if (nv <= 16) return launch_rows_vec<FMT, ROUND, 16>(x, ldx, rows, k, q, ldq, scales, st);
-        if (nv <= 24) return launch_rows_vec<FMT, ROUND, 24>(x, ldx, rows, k, q, ldq, scales, st);
-        if (nv <= 32) return launch_rows_vec<FMT, ROUND, 32>(x, ldx, rows, k, q, ldq, scales, st);
+        if (nv <= 2) return launch_rows_vec<FMT, ROUND, 2, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+        if (nv <= 4) return launch_rows_vec<FMT, ROUND, 4, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+        if (nv <= 8) return launch_rows_vec<FMT, ROUND, 8, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+        if (nv <= 12) return launch_rows_vec<FMT, ROUND, 12, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+        if (nv <= 16) return launch_rows_vec<FMT, ROUND, 16, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+        if (nv <= 24) return launch_rows_vec<FMT, ROUND, 24, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+        if (nv <= 32) return launch_rows_vec<FMT, ROUND, 32, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
     }
-    hipLaunchKernelGGL((quant_rows_any_kernel<FMT, ROUND>), dim3((unsigned)rows), dim3(256), 0, st, x, ldx, rows,
-                       k, q, ldq, scales);
+    hipLaunchKernelGGL((quant_rows_any_kernel<FMT, ROUND, TILED>), dim3((unsigned)rows), dim3(256), 0, st, x, ldx,
+                       rows, k, q, ldq, row0, scales);
     return hipGetLastError();
+}
+
+template <bool TILED>
+static hipError_t launch_quant_rows_layout(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, int fmt,
+                                           int rounding, uint8_t* q, int64_t ldq, int64_t row0, float* scales,
+                                           hipStream_t st) {
+    if (fmt == kFmtE4M3) return dispatch_rows<kFmtE4M3, kRoundDiv, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+    if (rounding == kRoundDiv)
+        return dispatch_rows<kFmtInt8, kRoundDiv, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+    return dispatch_rows<kFmtInt8, kRoundRcpMul, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
 }
 
 hipError_t launch_quant_rows(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, int fmt, int rounding,
                              uint8_t* q, int64_t ldq, float* scales, hipStream_t st) {
-    if (fmt == kFmtE4M3) return dispatch_rows<kFmtE4M3, kRoundDiv>(x, ldx, rows, k, q, ldq, scales, st);
-    if (rounding == kRoundDiv) return dispatch_rows<kFmtInt8, kRoundDiv>(x, ldx, rows, k, q, ldq, scales, st);
-    return dispatch_rows<kFmtInt8, kRoundRcpMul>(x, ldx, rows, k, q, ldq, scales, st);
+    return launch_quant_rows_layout<false>(x, ldx, rows, k, fmt, rounding, q, ldq, 0, scales, st);
+}
+
+hipError_t launch_quant_rows_tiled(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, int fmt, int rounding,
+                                   uint8_t* q_tiled, int64_t row0, float* scales, hipStream_t st) {
+    return launch_quant_rows_layout<true>(x, ldx, rows, k, fmt, rounding, q_tiled, k / 128, row0, scales, st);
 }
 
 // ---------------------------------------------------------------- per-tensor

@@ -34,7 +34,7 @@ bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
 extern "C" {
 
-__attribute__((visibility("default"))) int h3q_version(void) { return 100; }
+__attribute__((visibility("default"))) int h3q_version(void) { return 200; }
 
 __attribute__((visibility("default"))) const char* h3q_last_error(void) { return g_error; }
 
@@ -58,6 +58,34 @@ __attribute__((visibility("default"))) int h3q_quant_rows(const void* x, int64_t
                         "h3q_quant_rows");
 }
 
+__attribute__((visibility("default"))) int64_t h3q_tiled_bytes(int64_t rows, int64_t cols) {
+    if (rows <= 0 || cols <= 0 || cols % 128) return 0;
+    return (rows + 15) / 16 * (cols / 128) * 2048;
+}
+
+__attribute__((visibility("default"))) int h3q_quant_rows_tiled(const void* x, int64_t rows, int64_t cols,
+                                                                int64_t ldx, int format, int rounding, int64_t row0,
+                                                                void* codes_tiled, float* scales, void* stream) {
+    const char* who = "h3q_quant_rows_tiled";
+    if (rows < 0 || cols <= 0 || row0 < 0)
+        return fail(H3Q_ERR_INVALID, "%s: bad shape rows=%lld cols=%lld row0=%lld", who, (long long)rows,
+                    (long long)cols, (long long)row0);
+    if (cols % 128) return fail(H3Q_ERR_INVALID, "%s: cols=%lld must be a multiple of 128", who, (long long)cols);
+    if (format != H3Q_FMT_E4M3FN && format != H3Q_FMT_INT8)
+        return fail(H3Q_ERR_INVALID, "%s: unknown format %d", who, format);
+    if (rounding != H3Q_ROUND_DIV && rounding != H3Q_ROUND_RCP_MUL)
+        return fail(H3Q_ERR_INVALID, "%s: unknown rounding %d", who, rounding);
+    if (format == H3Q_FMT_E4M3FN && rounding != H3Q_ROUND_DIV)
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: e4m3fn codes use the division form only", who);
+    if (ldx < cols) return fail(H3Q_ERR_INVALID, "%s: leading dimension below cols", who);
+    if (rows == 0) return ok();
+    if (!x || !codes_tiled || !scales) return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
+    if (!aligned(codes_tiled, 16)) return fail(H3Q_ERR_INVALID, "%s: tiled codes must be 16-byte aligned", who);
+    return check_launch(h3q::launch_quant_rows_tiled((const uint16_t*)x, ldx, rows, cols, format, rounding,
+                                                     (uint8_t*)codes_tiled, row0, scales, (hipStream_t)stream),
+                        who);
+}
+
 __attribute__((visibility("default"))) int64_t h3q_quant_tensor_workspace_floats(int64_t rows, int64_t cols) {
     if (rows <= 0 || cols <= 0) return 1;
     return h3q::tensor_quant_parts(rows, cols);
@@ -79,31 +107,42 @@ __attribute__((visibility("default"))) int h3q_quant_tensor_e4m3(const void* x, 
 }
 
 static int check_gemm_operands(const char* who, const void* a, int64_t lda, const void* b, int64_t ldb, int64_t m,
-                               int64_t n, int64_t k, int64_t elem) {
+                               int64_t n, int64_t k, int64_t elem, bool a_tiled = false, bool b_tiled = false) {
     if (m < 0 || n < 0 || k < 0) return fail(H3Q_ERR_INVALID, "%s: negative shape", who);
     if (k % 16) return fail(H3Q_ERR_INVALID, "%s: k=%lld must be a multiple of 16", who, (long long)k);
-    if (lda < k * elem || ldb < k * elem) return fail(H3Q_ERR_INVALID, "%s: leading dimension below k", who);
-    if (lda % 16 || ldb % 16) return fail(H3Q_ERR_INVALID, "%s: lda/ldb must be multiples of 16 bytes", who);
+    if ((a_tiled || b_tiled) && k % 128)
+        return fail(H3Q_ERR_INVALID, "%s: tiled operands need k=%lld to be a multiple of 128", who, (long long)k);
+    if ((!a_tiled && lda < k * elem) || (!b_tiled && ldb < k * elem))
+        return fail(H3Q_ERR_INVALID, "%s: leading dimension below k", who);
+    if ((!a_tiled && lda % 16) || (!b_tiled && ldb % 16))
+        return fail(H3Q_ERR_INVALID, "%s: lda/ldb must be multiples of 16 bytes", who);
     if (!aligned(a, 16) || !aligned(b, 16)) return fail(H3Q_ERR_INVALID, "%s: a/b must be 16-byte aligned", who);
     // Block-relative buffer offsets are 32-bit: 256 rows of the larger stride must stay below 2^31.
-    if (lda >= (int64_t(1) << 23) || ldb >= (int64_t(1) << 23))
+    if ((!a_tiled && lda >= (int64_t(1) << 23)) || (!b_tiled && ldb >= (int64_t(1) << 23)))
         return fail(H3Q_ERR_UNSUPPORTED, "%s: row stride above 8 MiB", who);
     if ((m + 255) / 256 * ((n + 255) / 256) >= (int64_t(1) << 31))
         return fail(H3Q_ERR_UNSUPPORTED, "%s: too many output tiles", who);
     return H3Q_OK;
 }
 
-__attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void* a, int64_t lda,
+__attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void* a, int64_t lda, int a_layout,
                                                          const float* a_scale, int a_scale_kind, const void* b,
-                                                         int64_t ldb, const float* b_scale, int b_scale_kind,
-                                                         const void* bias, const void* lora_t, int64_t ldt,
-                                                         const void* lora_b, int64_t ldlb, int64_t lora_rank,
-                                                         float lora_scale, void* out, int64_t ldo, int64_t m,
-                                                         int64_t n, int64_t k, void* stream) {
+                                                         int64_t ldb, int b_layout, const float* b_scale,
+                                                         int b_scale_kind, const void* bias, const void* lora_t,
+                                                         int64_t ldt, const void* lora_b, int64_t ldlb,
+                                                         int64_t lora_rank, float lora_scale, void* out,
+                                                         int64_t ldo, int64_t m, int64_t n, int64_t k, void* stream) {
     const char* who = "h3q_scaled_mm";
     if (format != H3Q_FMT_E4M3FN && format != H3Q_FMT_INT8)
         return fail(H3Q_ERR_INVALID, "%s: unknown format %d", who, format);
-    if (int rc = check_gemm_operands(who, a, lda, b, ldb, m, n, k, 1)) return rc;
+    for (int layout : {a_layout, b_layout})
+        if (layout != H3Q_LAYOUT_ROWS && layout != H3Q_LAYOUT_TILED)
+            return fail(H3Q_ERR_INVALID, "%s: unknown operand layout %d", who, layout);
+    const bool a_tiled = a_layout == H3Q_LAYOUT_TILED, b_tiled = b_layout == H3Q_LAYOUT_TILED;
+    if (int rc = check_gemm_operands(who, a, lda, b, ldb, m, n, k, 1, a_tiled, b_tiled)) return rc;
+    if (a_tiled && (m > h3q::kSkinnyMaxM || lora_t))
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: tiled activations need m <= %lld and no LoRA", who,
+                    (long long)h3q::kSkinnyMaxM);
     for (int kind : {a_scale_kind, b_scale_kind})
         if (kind != H3Q_SCALE_PER_ROW && kind != H3Q_SCALE_PER_TENSOR)
             return fail(H3Q_ERR_INVALID, "%s: unknown scale kind %d", who, kind);
@@ -143,6 +182,8 @@ __attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void*
     g.lora_scale = lora_scale;
     g.out = out;
     g.ldo = ldo;
+    g.a_tiled = a_tiled;
+    g.b_tiled = b_tiled;
     const int kind = format == H3Q_FMT_E4M3FN ? h3q::kOpE4M3 : h3q::kOpInt8;
     return check_launch(h3q::launch_gemm(kind, false, g, (hipStream_t)stream), who);
 }

@@ -106,39 +106,6 @@ struct Tile {
     }
 };
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// Buffer descriptor of an operand region (4 SGPRs): base, stride 0, size in
-// bytes (offsets at or beyond it read as zero), raw-buffer format word.
-struct CopySrc {
-    v4i d;
-    __device__ __forceinline__ CopySrc(const void* base, uint32_t bytes) {
-        const uint64_t b = (uint64_t)base;
-        d = v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)b),
-                __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32) & 0xFFFF),
-                __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
-    }
-};
-
-// One wave-wide 16-byte-per-lane copy global -> LDS (buffer_load_dwordx4 ...
-// lds): lane L's 16 bytes at src + voff land at LDS byte lds_base + 16 L.
-// Issued as inline asm so the compiler's wait-count pass, which cannot tell
-// that the ring buffer being filled differs from the one being read, does not
-// insert a vmcnt(0) before every LDS read; the kernel waits for its copies
-// explicitly (wait_vmcnt + ring_barrier).  M0 carries the LDS base; nothing
-// else in these kernels uses M0.
-__device__ __forceinline__ void copy16(const CopySrc& src, uint32_t lds_base, uint32_t voff) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(lds_base), "v"(voff), "s"(src.d)
-                 : "memory");
-}
-
 // Copy rows [0, ROWS) x bytes [k0, k0 + BK) of an operand into an LDS stage.
 template <class T, int ROWS>
 __device__ __forceinline__ void load_tile(const CopySrc& rsrc, H3Q_LDS uint8_t* dst, uint32_t ld,
@@ -171,12 +138,49 @@ __device__ __forceinline__ typename Mfma<OP>::frag_t read_frag(const H3Q_LDS uin
     }
 }
 
+// Tiled operand (16-row x 128-byte blocks of 2 KiB in MFMA fragment order,
+// see code_offset in act_quant.hip): stage kt of a BN-row tile is BN / 16
+// blocks, each two 1 KiB halves, copied contiguously (block b, half h at LDS
+// byte (2 b + h) * 1024).  Rows past N are whole blocks past the descriptor.
+template <class T, int ROWS>
+__device__ __forceinline__ void load_tile_tiled(const CopySrc& rsrc, H3Q_LDS uint8_t* dst, int64_t steps, int kt,
+                                                int64_t nblk, int wave, int lane) {
+    static_assert(T::BK == 128, "tiled operands come in 128-byte k-steps");
+#pragma unroll
+    for (int i = 0; i < ROWS * 128 / 1024 / T::NWAVES; ++i) {
+        const int c = wave + T::NWAVES * i;
+        const int blk = c >> 1;
+        const uint32_t off = blk < nblk ? (uint32_t)(((int64_t)blk * steps + kt) * 2048 + (c & 1) * 1024 + 16 * lane)
+                                        : 0x80000000u;
+        copy16(rsrc, (uint32_t)(uintptr_t)(dst + c * 1024), off);
+    }
+}
+
+// Fragment of row `row` for k-step s from a tiled stage: its bytes k = kStep * s
+// + (fragment bytes) * g live in block row / 16, lane slot row % 16 + 16 q of
+// the 128-byte step (q = k / 32), halves 1 KiB apart.  Sixteen consecutive
+// rows read 16 consecutive 16-byte slots: no bank conflicts.
+template <int OP>
+__device__ __forceinline__ typename Mfma<OP>::frag_t read_frag_tiled(const H3Q_LDS uint8_t* tile, int row, int s,
+                                                                     int g) {
+    const H3Q_LDS uint8_t* blk = tile + (row >> 4) * 2048;
+    if constexpr (OP == kOpE4M3) {
+        const int slot = (row & 15) + 16 * (2 * s + g);
+        const v4i lo = *(const H3Q_LDS v4i*)(blk + 16 * slot);
+        const v4i hi = *(const H3Q_LDS v4i*)(blk + 1024 + 16 * slot);
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+        const int slot = (row & 15) + 16 * s;
+        return *(const H3Q_LDS v4i*)(blk + g * 1024 + 16 * slot);
+    }
+}
+
 // One stage of MFMAs.  The weight fragment is the MFMA's A operand and the
 // activation fragment its B operand, so accumulator tile acc[i][j] holds
 // out^T: lane L owns output row m = 32 i + L % 32 and, in accumulator slot v,
 // column n = 32 j + 8 (v / 4) + 4 (L / 32) + v % 4 -- four consecutive
 // columns per slot group, which the epilogue writes as one 8-byte store.
-template <class T, int OP>
+template <class T, int OP, bool TB>
 __device__ __forceinline__ void mma_stage(const H3Q_LDS uint8_t* sa, const H3Q_LDS uint8_t* sb, int wm0, int wn0,
                                           int lane, typename Mfma<OP>::acc_t (&acc)[T::TM][T::TN]) {
     constexpr int kSteps = T::BK / Mfma<OP>::kStep;
@@ -187,7 +191,8 @@ __device__ __forceinline__ void mma_stage(const H3Q_LDS uint8_t* sa, const H3Q_L
 #pragma unroll
         for (int i = 0; i < T::TM; ++i) af[i] = read_frag<T, OP>(sa, wm0 + 32 * i + r, s, g);
 #pragma unroll
-        for (int j = 0; j < T::TN; ++j) bfr[j] = read_frag<T, OP>(sb, wn0 + 32 * j + r, s, g);
+        for (int j = 0; j < T::TN; ++j)
+            bfr[j] = TB ? read_frag_tiled<OP>(sb, wn0 + 32 * j + r, s, g) : read_frag<T, OP>(sb, wn0 + 32 * j + r, s, g);
 #pragma unroll
         for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -242,7 +247,7 @@ __device__ __forceinline__ void wait_stage(int pending) {
 // branch: VEC (4 columns per store; needs ldo % 4 == 0, n % 4 == 0 and a
 // 16-byte aligned output) and BIAS.  The scalar-store variant (VEC = false)
 // takes the bias from a runtime check.
-template <class T, int OP, int EPI, bool LORA, bool VEC, bool BIAS>
+template <class T, int OP, int EPI, bool LORA, bool VEC, bool BIAS, bool TB>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int tiles_m, int tiles_n) {
     constexpr int BM = T::BM, BN = T::BN, BK = T::BK, S = T::STAGES, TM = T::TM, TN = T::TN;
     using acc_t = typename Mfma<OP>::acc_t;
@@ -263,7 +268,10 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
     const int64_t rows_a = (p.m - m0) < BM ? (p.m - m0) : BM;
     const int64_t rows_b = (p.n - n0) < BN ? (p.n - n0) : BN;
     const CopySrc ra((const uint8_t*)p.a + m0 * p.lda, (uint32_t)(rows_a * p.lda));
-    const CopySrc rb((const uint8_t*)p.b + n0 * p.ldb, (uint32_t)(rows_b * p.ldb));
+    const int64_t steps = kbytes / 128;                    // tiled B: 128-byte k-steps
+    const int64_t nblk = (rows_b + 15) / 16;               // tiled B: 16-row blocks in this tile
+    const CopySrc rb(TB ? (const uint8_t*)p.b + (n0 / 16) * steps * 2048 : (const uint8_t*)p.b + n0 * p.ldb,
+                     TB ? (uint32_t)(nblk * steps * 2048) : (uint32_t)(rows_b * p.ldb));
 
     // Scales are fetched before the main loop so their latency hides behind
     // it: each lane's row scales in registers, the block's column scales and
@@ -295,7 +303,8 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
     auto issue = [&](int kt, int buf) {
         H3Q_LDS uint8_t* dst = lds + buf * T::STAGE_BYTES;
         load_tile<T, BM>(ra, dst, (uint32_t)p.lda, (int64_t)kt * BK, kbytes, wave, lane);
-        load_tile<T, BN>(rb, dst + BM * BK, (uint32_t)p.ldb, (int64_t)kt * BK, kbytes, wave, lane);
+        if constexpr (TB) load_tile_tiled<T, BN>(rb, dst + BM * BK, steps, kt, nblk, wave, lane);
+        else load_tile<T, BN>(rb, dst + BM * BK, (uint32_t)p.ldb, (int64_t)kt * BK, kbytes, wave, lane);
     };
 #pragma unroll
     for (int s = 0; s < S - 1; ++s)
@@ -306,7 +315,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
         ring_barrier();
         issue(kt + S - 1, wr);
         const H3Q_LDS uint8_t* cur = lds + rd * T::STAGE_BYTES;
-        mma_stage<T, OP>(cur, cur + BM * BK, wm0, wn0, lane, acc);
+        mma_stage<T, OP, TB>(cur, cur + BM * BK, wm0, wn0, lane, acc);
         rd = rd + 1 == S ? 0 : rd + 1;
         wr = wr + 1 == S ? 0 : wr + 1;
     }
@@ -314,7 +323,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
         wait_stage<T>(ktiles - 1 - kt);
         ring_barrier();
         const H3Q_LDS uint8_t* cur = lds + rd * T::STAGE_BYTES;
-        mma_stage<T, OP>(cur, cur + BM * BK, wm0, wn0, lane, acc);
+        mma_stage<T, OP, TB>(cur, cur + BM * BK, wm0, wn0, lane, acc);
         rd = rd + 1 == S ? 0 : rd + 1;
     }
 
@@ -420,8 +429,16 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
 template <class T, int OP, int EPI, bool LORA, bool VEC, bool BIAS>
 hipError_t launch_tile(const GemmArgs& a, hipStream_t st) {
     const int tiles_m = (int)((a.m + T::BM - 1) / T::BM), tiles_n = (int)((a.n + T::BN - 1) / T::BN);
-    hipLaunchKernelGGL((gemm_kernel<T, OP, EPI, LORA, VEC, BIAS>), dim3((unsigned)(tiles_m * tiles_n)), dim3(T::NT), 0,
-                       st, a, tiles_m, tiles_n);
+    const dim3 grid((unsigned)(tiles_m * tiles_n));
+    if constexpr (OP != kOpBF16 && T::BK == 128) {
+        if (a.b_tiled) {
+            hipLaunchKernelGGL((gemm_kernel<T, OP, EPI, LORA, VEC, BIAS, true>), grid, dim3(T::NT), 0, st, a, tiles_m,
+                               tiles_n);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((gemm_kernel<T, OP, EPI, LORA, VEC, BIAS, false>), grid, dim3(T::NT), 0, st, a, tiles_m,
+                       tiles_n);
     return hipGetLastError();
 }
 
@@ -445,6 +462,7 @@ hipError_t launch_gemm(int kind, bool raw_i32, const GemmArgs& args, hipStream_t
     GemmArgs a = args;
     a.out_vec = (a.ldo % 4 == 0) && (a.n % 4 == 0) && ((uintptr_t)a.out % 16 == 0);
     const bool lora = a.lora_t != nullptr;
+    if (kind != kOpBF16 && !raw_i32 && skinny_supported(a)) return launch_gemm_skinny(kind, a, st);
     if (kind == kOpE4M3)
         return lora ? launch_scaled<TileBig, kOpE4M3, true>(a, st) : launch_scaled<TileBig, kOpE4M3, false>(a, st);
     if (kind == kOpInt8) {

@@ -68,4 +68,38 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 __device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Buffer descriptor of an operand region (4 SGPRs): base, stride 0, size in
+// bytes (offsets at or beyond it read as zero), raw-buffer format word.
+struct CopySrc {
+    v4i d;
+    __device__ __forceinline__ CopySrc(const void* base, uint32_t bytes) {
+        const uint64_t b = (uint64_t)base;
+        d = v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)b),
+                __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32) & 0xFFFF),
+                __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+    }
+};
+
+// One wave-wide 16-byte-per-lane copy global -> LDS (buffer_load_dwordx4 ...
+// lds): lane L's 16 bytes at src + voff land at LDS byte lds_base + 16 L.
+// Issued as inline asm so the compiler's wait-count pass, which cannot tell
+// that the ring buffer being filled differs from the one being read, does not
+// insert a vmcnt(0) before every LDS read; the kernel waits for its copies
+// explicitly (wait_vmcnt + ring_barrier).  M0 carries the LDS base; nothing
+// else in these kernels uses M0.
+__device__ __forceinline__ void copy16(const CopySrc& src, uint32_t lds_base, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(src.d)
+                 : "memory");
+}
+
+
 }  // namespace h3q

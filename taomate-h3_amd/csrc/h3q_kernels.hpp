@@ -10,6 +10,11 @@ namespace h3q {
 hipError_t launch_quant_rows(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, int fmt, int rounding,
                              uint8_t* q, int64_t ldq, float* scales, hipStream_t st);
 
+// Rows [row0, row0 + rows) of a K-column matrix into the tiled weight layout
+// (K % 128 == 0; see code_offset in act_quant.hip); scales[i] is row row0 + i.
+hipError_t launch_quant_rows_tiled(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, int fmt, int rounding,
+                                   uint8_t* q_tiled, int64_t row0, float* scales, hipStream_t st);
+
 int64_t tensor_quant_parts(int64_t rows, int64_t k);
 
 hipError_t launch_quant_tensor_e4m3(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k,
@@ -37,11 +42,18 @@ struct GemmArgs {
     void* out;              // bf16 [m, n] or int32 [m, n]
     int64_t ldo;            // in elements
     int out_vec;            // ldo % 4 == 0, n % 4 == 0 and out 16-byte aligned: 4 columns per store
+    int a_tiled, b_tiled;   // operand stored in the tiled layout (k % 128 == 0; rows padded to 16 with zeros)
 };
 
 // out = epilogue(A @ B^T).  kind: kOpE4M3 / kOpInt8 scaled to bf16 (with
 // optional bias and LoRA); raw_i32: int8 accumulators written as int32;
 // kOpBF16: plain bf16 GEMM (LoRA down-projection).
 hipError_t launch_gemm(int kind, bool raw_i32, const GemmArgs& args, hipStream_t st);
+
+// Weight-streaming GEMM for M <= kSkinnyMaxM activation rows (scaled e4m3 /
+// int8 to bf16, optional bias, no LoRA).  launch_gemm routes there itself.
+constexpr int64_t kSkinnyMaxM = 128;
+bool skinny_supported(const GemmArgs& a);
+hipError_t launch_gemm_skinny(int kind, const GemmArgs& a, hipStream_t st);
 
 }  // namespace h3q

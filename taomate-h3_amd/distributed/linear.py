@@ -59,8 +59,9 @@ def _fp8_w8a8_linear(inputs: torch.Tensor, weight: torch.Tensor, weight_scale: t
     """Per-token dynamic e4m3fn activations x per-channel e4m3fn weights."""
     shape = (*inputs.shape[:-1], int(weight.shape[0]))
     flat = inputs.reshape(-1, int(inputs.shape[-1])).contiguous()
-    q, s = ops.quant_rows(flat, ops.FMT_E4M3FN, ops.ROUND_DIV)
-    out = ops.scaled_mm(q, weight, s.reshape(-1), weight_scale.reshape(-1), bias=bias)
+    q, s, a_tiled = ops.quant_activations_for(flat, ops.FMT_E4M3FN, ops.ROUND_DIV, weight)
+    out = ops.scaled_mm(q, weight, s.reshape(-1), weight_scale.reshape(-1), bias=bias, a_tiled=a_tiled,
+                        b_tiled=ops.is_tiled(weight), m=int(flat.shape[0]))
     return out.reshape(shape)
 
 

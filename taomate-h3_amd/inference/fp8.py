@@ -272,7 +272,8 @@ def quantize_h3_block_linears_fp8_w8a8_(torch: Any, transformer: Any, *, policy:
     """Per-output-channel e4m3fn weights + dynamic per-token e4m3fn activations
     for the selected block linears (no counterpart in the reference; the
     format of the BASELINE FP8 W8A8 configurations).  Bias is kept (bf16) and
-    fused into the GEMM epilogue."""
+    fused into the GEMM epilogue.  Weights with N % 16 == 0 and K % 128 == 0
+    are stored in the tiled layout (``weight._h3q_tiled``)."""
     candidates = _block_candidates(transformer, (".attn.qkv_proj", ".attn.out_proj", ".mlp.fc1", ".mlp.fc2"))
     if not candidates:
         raise RuntimeError("no H3 DiT block linears were selected for FP8 W8A8")
@@ -285,10 +286,16 @@ def quantize_h3_block_linears_fp8_w8a8_(torch: Any, transformer: Any, *, policy:
         weight = module.weight.detach()
         if weight.dtype != torch.bfloat16:
             raise TypeError(f"{name} expected BF16 weight before FP8 W8A8 conversion")
-        quantized, scale = quantize_weight_fp8_rows(weight)
+        tiled = ops.can_tile(int(weight.shape[0]), int(weight.shape[1]))
+        if tiled:
+            quantized, scale = ops.quant_rows_tiled(weight.contiguous(), ops.FMT_E4M3FN, ops.ROUND_DIV)
+        else:
+            quantized, scale = quantize_weight_fp8_rows(weight)
         source_bytes += int(weight.numel() * weight.element_size())
         quantized_bytes += int(quantized.numel() * quantized.element_size())
         module.weight = torch.nn.Parameter(quantized, requires_grad=False)
+        if tiled:
+            ops.mark_tiled(module.weight)
         module.register_buffer("_fp8_w8a8_weight_scale", scale, persistent=False)
         names.append(name)
     if not names:

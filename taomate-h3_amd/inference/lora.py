@@ -64,7 +64,8 @@ def fused_quantized_lora_linear(base: Any, inputs: torch.Tensor, lora_a: torch.T
         out = None
         w_scale = base._fp8_w8a8_weight_scale
     out = ops.scaled_mm(q, base.weight, s.reshape(-1), w_scale.reshape(-1), bias=bias, lora_t=t,
-                        lora_b=lora_b.contiguous(), lora_scale=float(scale), out=out)
+                        lora_b=lora_b.contiguous(), lora_scale=float(scale), out=out,
+                        b_tiled=ops.is_tiled(base.weight))
     return out.reshape(shape)
 
 

@@ -13,10 +13,14 @@ CUDA operators replaced by the gfx950 library (include/taomate_h3_amd.h):
 * ``CutlassW8A8Workspace`` (w8a8.py:136-187) keeps the grow-only per
   (device, stream, width) buffers and the aliasing of same-width outputs.
 
-Module state is unchanged: ``weight`` int8 ``[N, K]`` (row-major, the
-``nn.Linear`` layout, consumed directly -- the kernel reads ``weight`` where
-vLLM read ``weight.t()``), ``_cutlass_w8a8_weight_scale`` fp32 ``[N, 1]``
+Module state keeps the reference's names, shapes and byte counts:
+``weight`` int8 ``[N, K]``, ``_cutlass_w8a8_weight_scale`` fp32 ``[N, 1]``
 (non-persistent), the stream-load flags and the optional workspace views.
+When N % 16 == 0 and K % 128 == 0 (every H3 projection) the codes in
+``weight`` are stored in the GEMMs' tiled layout (16-row x 128-byte MFMA
+fragment tiles, include/taomate_h3_amd.h) and the parameter carries
+``_h3q_tiled = True``; otherwise they are row-major.  The tiled writer
+quantizes straight into that layout, row chunk by row chunk.
 """
 
 from __future__ import annotations
@@ -107,6 +111,8 @@ def prepare_cutlass_w8a8_stream_load_slot_(module: Any, *, name: str) -> None:
         raise RuntimeError(f"{name} expected a bias-free H3 projection")
     module.weight = torch.nn.Parameter(torch.empty(weight.shape, dtype=torch.int8, device=weight.device),
                                        requires_grad=False)
+    if ops.can_tile(int(weight.shape[0]), int(weight.shape[1])):
+        ops.mark_tiled(module.weight)
     module.register_buffer("_cutlass_w8a8_weight_scale",
                            torch.empty((int(weight.shape[0]), 1), dtype=torch.float32, device=weight.device),
                            persistent=False)
@@ -132,11 +138,16 @@ def load_cutlass_w8a8_stream_weight_(module: Any, source_weight: torch.Tensor, *
     rows_per_chunk = max(1, maximum_temporary_bytes // (int(source_weight.shape[1]) * source_weight.element_size()))
     weight = module.weight
     scale = module._cutlass_w8a8_weight_scale
+    tiled = ops.is_tiled(weight)
     for start in range(0, int(source_weight.shape[0]), rows_per_chunk):
         stop = min(start + rows_per_chunk, int(source_weight.shape[0]))
         temporary = source_weight[start:stop].to(device=weight.device, dtype=torch.bfloat16)
-        ops.quant_rows(temporary, ops.FMT_INT8, ops.ROUND_DIV, codes=weight.data[start:stop],
-                       scales=scale[start:stop])
+        if tiled:
+            ops.quant_rows_tiled(temporary, ops.FMT_INT8, ops.ROUND_DIV, codes=weight.data, row0=start,
+                                 scales=scale[start:stop])
+        else:
+            ops.quant_rows(temporary, ops.FMT_INT8, ops.ROUND_DIV, codes=weight.data[start:stop],
+                           scales=scale[start:stop])
     module._cutlass_w8a8_stream_load_temporary_bytes_limit = int(maximum_temporary_bytes)
     module._cutlass_w8a8_stream_load_pending = False
     module._cutlass_w8a8_stream_loaded = True
@@ -163,13 +174,15 @@ class CutlassW8A8Workspace:
         return inputs.device.index, int(stream.cuda_stream)
 
     def buffers(self, inputs: torch.Tensor, output_width: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        """(codes [M, K] int8, scales [M, 1] fp32, out [M, N] bf16) views for this call."""
+        """(codes [M, K] int8, scales [M, 1] fp32, out [M, N] bf16) views for this call.
+        The codes buffer holds at least ops.tiled_rows(M) rows (the tiled
+        layout pads to 16); ``_codes_buffer`` returns it whole."""
         rows, width = int(inputs.shape[0]), int(inputs.shape[1])
         device_index, stream = self._stream(inputs)
         key = (device_index, stream, width)
         act = self._activation.get(key)
-        if act is None or int(act[0].shape[0]) < rows:
-            act = (torch.empty((rows, width), device=inputs.device, dtype=torch.int8),
+        if act is None or int(act[1].shape[0]) < rows:
+            act = (torch.empty((ops.tiled_rows(rows), width), device=inputs.device, dtype=torch.int8),
                    torch.empty((rows, 1), device=inputs.device, dtype=torch.float32))
             self._activation[key] = act
         out_key = (device_index, stream, int(output_width))
@@ -179,10 +192,18 @@ class CutlassW8A8Workspace:
             self._outputs[out_key] = out
         return act[0][:rows], act[1][:rows], out[:rows]
 
+    def _codes_buffer(self, inputs: torch.Tensor) -> torch.Tensor:
+        device_index, stream = self._stream(inputs)
+        return self._activation[(device_index, stream, int(inputs.shape[1]))][0]
+
     def linear(self, inputs: torch.Tensor, weight_t: torch.Tensor, weight_scale_t: torch.Tensor) -> torch.Tensor:
-        quantized, activation_scale, output = self.buffers(inputs, int(weight_t.shape[1]))
-        ops.quant_rows(inputs, ops.FMT_INT8, ops.ROUND_RCP_MUL, codes=quantized, scales=activation_scale)
-        ops.scaled_mm(quantized, weight_t.t(), activation_scale, weight_scale_t.reshape(-1), out=output)
+        rows = int(inputs.shape[0])
+        _, activation_scale, output = self.buffers(inputs, int(weight_t.shape[1]))
+        quantized, activation_scale, a_tiled = ops.quant_activations_for(
+            inputs, ops.FMT_INT8, ops.ROUND_RCP_MUL, weight_t, codes=self._codes_buffer(inputs),
+            scales=activation_scale)
+        ops.scaled_mm(quantized, weight_t.t(), activation_scale, weight_scale_t.reshape(-1), out=output,
+                      a_tiled=a_tiled, b_tiled=ops.is_tiled(weight_t), m=rows)
         return output
 
 
@@ -196,8 +217,17 @@ def cutlass_w8a8_linear(inputs: torch.Tensor, weight: torch.Tensor, weight_scale
     shape = (*inputs.shape[:-1], int(weight.shape[0]))
     flattened = inputs.reshape(-1, int(inputs.shape[-1])).contiguous()
     if workspace is not None:
-        output = workspace.linear(flattened, weight.t() if weight_t is None else weight_t,
-                                  weight_scale.t() if weight_scale_t is None else weight_scale_t)
+        if weight_t is None:
+            weight_t = weight.t()
+            if ops.is_tiled(weight):
+                ops.mark_tiled(weight_t)
+        output = workspace.linear(flattened, weight_t, weight_scale.t() if weight_scale_t is None else weight_scale_t)
+        return output.reshape(shape)
+    if ops.is_tiled(weight):
+        quantized, activation_scale, a_tiled = ops.quant_activations_for(flattened, ops.FMT_INT8, ops.ROUND_RCP_MUL,
+                                                                         weight)
+        output = ops.scaled_mm(quantized, weight, activation_scale.reshape(-1), weight_scale.reshape(-1),
+                               a_tiled=a_tiled, b_tiled=True, m=int(flattened.shape[0]))
         return output.reshape(shape)
     backend = require_vllm_cutlass_w8a8()
     quantized, activation_scale, _ = backend.scaled_int8_quant(flattened)
@@ -260,6 +290,8 @@ def enable_h3_cutlass_w8a8_workspace_(transformer: Any) -> dict[str, Any]:
     for module in selected:
         module._cutlass_w8a8_workspace = workspace
         module._cutlass_w8a8_weight_t = module.weight.t()
+        if ops.is_tiled(module.weight):
+            ops.mark_tiled(module._cutlass_w8a8_weight_t)
         module._cutlass_w8a8_weight_scale_t = module._cutlass_w8a8_weight_scale.t()
     return {
         "linear_count": len(selected),

@@ -20,6 +20,9 @@ ROUND_DIV = 0
 ROUND_RCP_MUL = 1
 SCALE_PER_TENSOR = 0
 SCALE_PER_ROW = 1
+LAYOUT_ROWS = 0
+LAYOUT_TILED = 1
+SKINNY_MAX_M = 128   # tiled activations (weight-streaming GEMM) up to this many rows
 
 _CODE_DTYPES = {FMT_E4M3FN: torch.float8_e4m3fn, FMT_INT8: torch.int8}
 _FORMATS = {torch.float8_e4m3fn: FMT_E4M3FN, torch.int8: FMT_INT8}
@@ -78,6 +81,80 @@ def quant_rows(x: torch.Tensor, fmt: int, rounding: int = ROUND_DIV, *, codes: t
     return codes, scales
 
 
+def can_tile(rows: int, cols: int) -> bool:
+    """Whether a [rows, cols] weight is stored tiled by the module mirror:
+    the tiled matrix then has exactly the row-major shape and byte count."""
+    return rows > 0 and rows % 16 == 0 and cols > 0 and cols % 128 == 0
+
+
+def is_tiled(t: torch.Tensor | None) -> bool:
+    """True for a code tensor (or a view object) marked as holding the tiled layout."""
+    return bool(getattr(t, "_h3q_tiled", False))
+
+
+def mark_tiled(t: torch.Tensor) -> torch.Tensor:
+    t._h3q_tiled = True
+    return t
+
+
+def quant_activations_for(x: torch.Tensor, fmt: int, rounding: int, weight: torch.Tensor, *,
+                          codes: torch.Tensor | None = None, scales: torch.Tensor | None = None):
+    """Per-token quantization of the 2-D activations of a linear whose weight
+    codes are ``weight``: tiled (for the weight-streaming GEMM) when the
+    weight is tiled and there are at most 128 tokens, else row-major.
+    Returns (codes, scales, a_tiled); ``codes`` may be a larger workspace
+    buffer of rows >= tiled_rows(m)."""
+    m, k = x.shape
+    if is_tiled(weight) and 0 < m <= SKINNY_MAX_M and k % 128 == 0:
+        buf = None if codes is None else codes[:tiled_rows(m)]
+        q, s = quant_rows_tiled(x, fmt, rounding, codes=buf, scales=scales)
+        return q, s, True
+    buf = None if codes is None else codes[:m]
+    q, s = quant_rows(x, fmt, rounding, codes=buf, scales=scales)
+    return q, s, False
+
+
+def tiled_rows(rows: int) -> int:
+    """Rows of storage a tiled operand of ``rows`` logical rows occupies (a multiple of 16)."""
+    return (int(rows) + 15) // 16 * 16
+
+
+def tiled_bytes(rows: int, cols: int) -> int:
+    """Bytes of the tiled layout of a [rows, cols] code matrix (cols % 128 == 0), else 0."""
+    return int(_lib.lib().h3q_tiled_bytes(int(rows), int(cols)))
+
+
+def quant_rows_tiled(x: torch.Tensor, fmt: int, rounding: int = ROUND_DIV, *, codes: torch.Tensor | None = None,
+                     row0: int = 0, scales: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row quantization of bf16 ``x [rows, K]`` into rows [row0, row0 + rows) of a tiled code matrix.
+
+    ``codes`` is the whole tiled matrix, a contiguous [R, K] tensor of the code
+    dtype with R a multiple of 16 (allocated here as [tiled_rows(rows), K]
+    when omitted, which requires row0 == 0).  Scales are returned for the
+    quantized rows only ([rows, 1] fp32)."""
+    _require_gpu("quant_rows_tiled", x, codes, scales)
+    _rows_2d("quant_rows_tiled x", x, torch.bfloat16)
+    rows, cols = x.shape
+    if cols % 128:
+        raise ValueError(f"quant_rows_tiled: K={cols} must be a multiple of 128")
+    if codes is None:
+        if row0:
+            raise ValueError("quant_rows_tiled: pass the tiled matrix when row0 > 0")
+        codes = torch.empty((tiled_rows(rows), cols), device=x.device, dtype=_CODE_DTYPES[fmt])
+    if codes.dtype != _CODE_DTYPES[fmt] or codes.ndim != 2 or codes.shape[1] != cols or not codes.is_contiguous():
+        raise ValueError("quant_rows_tiled: codes must be a contiguous [R, K] tensor of the code dtype")
+    if codes.shape[0] % 16 or row0 < 0 or row0 + rows > codes.shape[0]:
+        raise ValueError(f"quant_rows_tiled: rows [{row0}, {row0 + rows}) do not fit a tiled matrix of "
+                         f"{codes.shape[0]} rows (a multiple of 16)")
+    if scales is None:
+        scales = torch.empty((rows, 1), device=x.device, dtype=torch.float32)
+    if scales.dtype != torch.float32 or scales.numel() != rows or not scales.is_contiguous():
+        raise ValueError("quant_rows_tiled: scales must be a contiguous fp32 tensor with one entry per row")
+    _lib.call("h3q_quant_rows_tiled", _ptr(x), rows, cols, x.stride(0) if rows else cols, fmt, rounding, int(row0),
+              _ptr(codes), _ptr(scales), _stream(x))
+    return codes, scales
+
+
 def quant_tensor_e4m3(x: torch.Tensor, static_scale: torch.Tensor | None = None, *,
                       codes: torch.Tensor | None = None, scale: torch.Tensor | None = None,
                       workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
@@ -122,18 +199,28 @@ def _scale_kind(name: str, s: torch.Tensor, count: int) -> int:
 def scaled_mm(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor, b_scale: torch.Tensor, *,
               bias: torch.Tensor | None = None, lora_t: torch.Tensor | None = None,
               lora_b: torch.Tensor | None = None, lora_scale: float = 1.0,
-              out: torch.Tensor | None = None) -> torch.Tensor:
+              out: torch.Tensor | None = None, a_tiled: bool = False, b_tiled: bool = False,
+              m: int | None = None, n: int | None = None) -> torch.Tensor:
     """bf16 out[m, n] = a_scale[m] * (b_scale[n] * (a @ b^T)) [+ bias] [+ lora_scale * lora_t @ lora_b^T].
 
     ``a`` [m, k] and ``b`` [n, k] are both e4m3fn or both int8 codes (``b`` in
-    the nn.Linear [out, in] layout)."""
+    the nn.Linear [out, in] layout).  A tiled operand (``a_tiled`` /
+    ``b_tiled``, see quant_rows_tiled) is a contiguous [R, k] tensor with R the
+    row count rounded up to 16; ``m`` / ``n`` give the logical row counts when
+    they differ from R."""
     _require_gpu("scaled_mm", a, b, a_scale, b_scale, bias, lora_t, lora_b, out)
     if a.dtype not in _FORMATS or b.dtype != a.dtype:
         raise TypeError(f"scaled_mm: operands must both be e4m3fn or int8, got {a.dtype} and {b.dtype}")
     _rows_2d("scaled_mm a", a, a.dtype)
     _rows_2d("scaled_mm b", b, b.dtype)
-    m, k = a.shape
-    n = b.shape[0]
+    k = a.shape[1]
+    m = a.shape[0] if m is None else int(m)
+    n = b.shape[0] if n is None else int(n)
+    for name, t, rows, tiled in (("a", a, m, a_tiled), ("b", b, n, b_tiled)):
+        need = tiled_rows(rows) if tiled else rows
+        if t.shape[0] < need or (tiled and not t.is_contiguous()):
+            raise ValueError(f"scaled_mm: {name} holds {t.shape[0]} rows, {need} needed"
+                             + (" (tiled operands are contiguous, rows rounded up to 16)" if tiled else ""))
     if b.shape[1] != k:
         raise ValueError(f"scaled_mm: inner dimensions differ ({k} vs {b.shape[1]})")
     ak = _scale_kind("scaled_mm a_scale", a_scale, m)
@@ -157,8 +244,9 @@ def scaled_mm(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor, b_scale: 
         raise ValueError(f"scaled_mm: out shape {tuple(out.shape)} != {(m, n)}")
     if m == 0 or n == 0:
         return out
-    _lib.call("h3q_scaled_mm", _FORMATS[a.dtype], _ptr(a), a.stride(0), _ptr(a_scale), ak, _ptr(b), b.stride(0),
-              _ptr(b_scale), bk, _ptr(bias), _ptr(lora_t), lora_t.stride(0) if lora_t is not None else 0,
+    _lib.call("h3q_scaled_mm", _FORMATS[a.dtype], _ptr(a), a.stride(0), LAYOUT_TILED if a_tiled else LAYOUT_ROWS,
+              _ptr(a_scale), ak, _ptr(b), b.stride(0), LAYOUT_TILED if b_tiled else LAYOUT_ROWS, _ptr(b_scale), bk,
+              _ptr(bias), _ptr(lora_t), lora_t.stride(0) if lora_t is not None else 0,
               _ptr(lora_b), lora_b.stride(0) if lora_b is not None else 0, rank, float(lora_scale), _ptr(out),
               out.stride(0), m, n, k, _stream(a))
     return out

@@ -52,3 +52,13 @@ def bf16_ulp(v: np.ndarray) -> np.ndarray:
 def fp32_gemm_bound(k: int, abs_sum: np.ndarray) -> np.ndarray:
     """Worst-case error of a binary32 accumulation of k terms: k * 2^-24 * sum|terms|."""
     return k * 2.0 ** -24 * abs_sum
+
+
+def to_tiled(codes: np.ndarray) -> np.ndarray:
+    """Row-major [R, K] codes (R % 16 == 0, K % 128 == 0) -> the bytes of the
+    tiled layout, as an [R, K] array: 16-row x 128-byte blocks of 2 KiB, block
+    (b, s) at (b * K / 128 + s) * 2048, inside it byte k of row r at
+    (k % 32 // 16) * 1024 + (r % 16 + 16 * (k % 128 // 32)) * 16 + k % 16."""
+    r, k = codes.shape
+    c = np.ascontiguousarray(codes).reshape(r // 16, 16, k // 128, 4, 2, 16)  # b, r16, s, q, h, byte
+    return np.ascontiguousarray(c.transpose(0, 2, 4, 3, 1, 5)).reshape(r, k)  # b, s, h, q, r16, byte

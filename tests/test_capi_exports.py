@@ -22,7 +22,7 @@ def _declared() -> set[str]:
 def test_header_declares_entry_points():
     names = _declared()
     assert {"h3q_quant_rows", "h3q_quant_tensor_e4m3", "h3q_scaled_mm", "h3q_gemm_i8_i32",
-            "h3q_lora_down", "h3q_last_error", "h3q_version"} <= names
+            "h3q_lora_down", "h3q_last_error", "h3q_version", "h3q_tiled_bytes", "h3q_quant_rows_tiled"} <= names
 
 
 def test_library_exports_every_declared_symbol():
@@ -45,11 +45,24 @@ def test_version_and_error_without_gpu():
     if not _lib.LIB_PATH.exists():
         pytest.skip("library not built")
     lib = _lib.lib()
-    assert lib.h3q_version() >= 100
+    assert lib.h3q_version() >= 200
     # Argument errors are rejected on the host before any launch.
     rc = lib.h3q_quant_rows(None, 4, 16, 16, 7, 0, None, 16, None, None)
     assert rc == 1
     assert b"unknown format" in lib.h3q_last_error()
-    rc = lib.h3q_scaled_mm(0, None, 16, None, 1, None, 16, None, 1, None, None, 0, None, 0, 0, 1.0, None, 8,
+    rc = lib.h3q_scaled_mm(0, None, 16, 0, None, 1, None, 16, 0, None, 1, None, None, 0, None, 0, 0, 1.0, None, 8,
                            4, 8, 24, None)
     assert rc == 1 and b"multiple of 16" in lib.h3q_last_error()
+    # tiled operands: k must be a multiple of 128; tiled activations only for m <= 128 without LoRA
+    rc = lib.h3q_scaled_mm(0, None, 0, 0, None, 1, None, 0, 1, None, 1, None, None, 0, None, 0, 0, 1.0, None, 8,
+                           4, 8, 64, None)
+    assert rc == 1 and b"multiple of 128" in lib.h3q_last_error()
+    rc = lib.h3q_scaled_mm(0, None, 0, 1, None, 1, None, 0, 1, None, 1, None, None, 0, None, 0, 0, 1.0, None, 8,
+                           256, 8, 128, None)
+    assert rc == 2 and b"tiled activations" in lib.h3q_last_error()
+    rc = lib.h3q_scaled_mm(0, None, 128, 5, None, 1, None, 128, 0, None, 1, None, None, 0, None, 0, 0, 1.0, None,
+                           8, 4, 8, 128, None)
+    assert rc == 1 and b"unknown operand layout" in lib.h3q_last_error()
+    rc = lib.h3q_quant_rows_tiled(None, 4, 100, 100, 0, 0, 0, None, None, None)
+    assert rc == 1 and b"multiple of 128" in lib.h3q_last_error()
+    assert lib.h3q_tiled_bytes(17, 256) == 2 * 2 * 2048 and lib.h3q_tiled_bytes(16, 100) == 0

@@ -56,7 +56,8 @@ def test_int8_accumulator_extremes(ops, oracle, device):
 
 
 @pytest.mark.parametrize("bias", [False, True])
-@pytest.mark.parametrize("m,n,k", [(256, 1024, 1024), (100, 300, 2048), (640, 512, 5120)])
+@pytest.mark.parametrize("m,n,k", [(256, 1024, 1024), (100, 300, 2048), (640, 512, 5120),
+                                   (16, 512, 1040), (128, 1000, 5120), (3, 77, 528), (64, 5120, 5120)])
 def test_int8_scaled_bit_exact(ops, oracle, device, m, n, k, bias):
     x = activations(m, k, seed=m, outlier_channels=8)
     w = weights(n, k, seed=n)
@@ -164,7 +165,8 @@ def test_fp8_truncation_known_answers_through_gemm(ops, oracle, device):
 
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("m,n,k", [(256, 1024, 1024), (300, 200, 1040), (1, 256, 512), (640, 768, 5120),
-                                   (257, 511, 13824), (150, 512, 256)])
+                                   (257, 511, 13824), (150, 512, 256), (16, 5120, 5120), (64, 5120, 5120),
+                                   (128, 5120, 5120), (5, 300, 1040), (100, 262, 528), (33, 17, 16)])
 def test_fp8_scaled_matches_oracle(ops, oracle, device, m, n, k, bias):
     print(f"fp8 gemm {m}x{n}x{k} bias={bias}", flush=True)
     out, rqa, rsa, rqw, rsw, bb = _fp8_case(ops, oracle, device, m, n, k, seed=m + n + k, bias=bias)
@@ -241,3 +243,61 @@ def test_fp8_layout_identity(ops, device):
     torch.cuda.synchronize()
     expect = b.view(torch.float8_e4m3fn).float().t().to(torch.bfloat16)
     assert torch.equal(out.cpu(), expect)
+
+
+def _tiled_case(ops, oracle, device, m, n, k, fmt, a_tiled, bias, lora_rank=0, seed=3):
+    """Quantize with the tiled writer (weights always, activations if a_tiled)
+    and run the scaled GEMM on the tiled operands."""
+    f = ops.FMT_E4M3FN if fmt == "e4m3" else ops.FMT_INT8
+    x = activations(m, k, seed=seed, outlier_channels=max(1, k // 100), outlier_scale=15.0)
+    w = weights(n, k, seed=seed + 1)
+    xg, wg = x.to(device), w.to(device)
+    qw, sw = ops.quant_rows_tiled(wg, f, ops.ROUND_DIV)
+    ar = ops.ROUND_DIV if fmt == "e4m3" else ops.ROUND_RCP_MUL
+    if a_tiled:
+        qa, sa = ops.quant_rows_tiled(xg, f, ar)
+    else:
+        qa, sa = ops.quant_rows(xg, f, ar)
+    bvec = (torch.randn(n, generator=torch.Generator().manual_seed(seed + 2)) * 0.01).to(torch.bfloat16)
+    kw = {}
+    if lora_rank:
+        gen = torch.Generator().manual_seed(seed + 5)
+        la = (torch.randn(lora_rank, k, generator=gen) * 0.01).to(torch.bfloat16)
+        lb = (torch.randn(n, lora_rank, generator=gen) * 0.01).to(torch.bfloat16)
+        kw = dict(lora_t=ops.lora_down(xg, la.to(device)), lora_b=lb.to(device), lora_scale=0.5)
+    out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), bias=bvec.to(device) if bias else None,
+                        a_tiled=a_tiled, b_tiled=True, m=m, n=n, **kw)
+    ref_out = None
+    if lora_rank:   # same call on row-major operands: the layouts must not change a single bit
+        qa2, sa2 = ops.quant_rows(xg, f, ar)
+        qw2, sw2 = ops.quant_rows(wg, f, ops.ROUND_DIV)
+        ref_out = ops.scaled_mm(qa2, qw2, sa2.reshape(-1), sw2.reshape(-1), bias=bvec.to(device) if bias else None,
+                                **kw)
+    torch.cuda.synchronize()
+    rqa, rsa = oracle.quant_rows(bits16(x), fmt, "div" if fmt == "e4m3" else "rcp")
+    rqw, rsw = oracle.quant_rows(bits16(w), fmt, "div")
+    return out, ref_out, rqa, rsa, rqw, rsw, (bits16(bvec) if bias else None)
+
+
+@pytest.mark.parametrize("m,n,k,a_tiled", [(16, 5120, 5120, True), (16, 5120, 5120, False), (64, 512, 1024, True),
+                                           (5, 304, 1024, True), (100, 256, 2048, False), (128, 5120, 5120, True),
+                                           (300, 512, 1024, False), (640, 768, 5120, False),
+                                           (257, 528, 13824, False)])
+@pytest.mark.parametrize("fmt", ["e4m3", "int8"])
+def test_tiled_weight_gemm(ops, oracle, device, m, n, k, a_tiled, fmt):
+    """Tiled weights (and tiled activations for m <= 128) through the skinny
+    and the large GEMM: int8 bit-exact, e4m3 against the instruction model."""
+    print(f"tiled gemm {fmt} {m}x{n}x{k} a_tiled={a_tiled}", flush=True)
+    out, _, rqa, rsa, rqw, rsw, bb = _tiled_case(ops, oracle, device, m, n, k, fmt, a_tiled, bias=(m % 2 == 0))
+    if fmt == "int8":
+        ref = oracle.epilogue(oracle.gemm_i8_i32_fast(rqa, rqw), rsa, rsw, bb)
+        np.testing.assert_array_equal(bits16(out), ref)
+    else:
+        _assert_fp8_close(oracle, bits16(out), rqa, rsa, rqw, rsw, bb)
+
+
+def test_tiled_weight_lora_bias_matches_row_major(ops, oracle, device):
+    """Large GEMM with tiled weights, bias and the LoRA epilogue gives the
+    same bits as with row-major weights."""
+    out, ref_out, *_ = _tiled_case(ops, oracle, device, 300, 512, 1024, "e4m3", False, bias=True, lora_rank=64)
+    np.testing.assert_array_equal(bits16(out), bits16(ref_out))

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import activations, bits8, bits16, weights
+from _util import activations, bits8, bits16, to_tiled, weights
 from test_gpu_gemm import _assert_fp8_close
 
 pytestmark = pytest.mark.gpu
@@ -62,9 +62,11 @@ def test_quantize_weight_matches_reference_formula(oracle, device):
     np.testing.assert_array_equal(s.cpu().numpy().ravel(), rs)
 
 
-@pytest.mark.parametrize("rows,k,limit", [(300, 512, 1024 * 1024), (300, 512, 512 * 2 * 7), (5, 256, 1)])
+@pytest.mark.parametrize("rows,k,limit", [(300, 512, 1024 * 1024), (300, 512, 512 * 2 * 7), (5, 256, 1),
+                                         (320, 512, 512 * 2 * 7), (64, 1024, 1)])
 def test_stream_load_chunks_equal_whole_matrix(oracle, device, rows, k, limit):
-    """Bounded row chunks (w8a8.py:98-133) give the whole-matrix codes and scales."""
+    """Bounded row chunks (w8a8.py:98-133) give the whole-matrix codes and
+    scales; aligned shapes are written straight into the tiled layout."""
     w8a8 = _mod("inference.w8a8")
     m = torch.nn.Module()
     m.weight = torch.nn.Parameter(torch.empty(rows, k, dtype=torch.bfloat16, device=device))
@@ -74,7 +76,10 @@ def test_stream_load_chunks_equal_whole_matrix(oracle, device, rows, k, limit):
     w8a8.load_cutlass_w8a8_stream_weight_(m, src, name="blocks.2.mlp.fc1", maximum_temporary_bytes=limit)
     torch.cuda.synchronize()
     rq, rs = oracle.quant_rows(bits16(src), "int8", "div")
-    np.testing.assert_array_equal(bits8(m.weight).view(np.int8), rq)
+    tiled = rows % 16 == 0 and k % 128 == 0
+    assert getattr(m.weight, "_h3q_tiled", False) == tiled
+    expect = to_tiled(rq.view(np.uint8)) if tiled else rq.view(np.uint8)
+    np.testing.assert_array_equal(bits8(m.weight), expect)
     np.testing.assert_array_equal(m._cutlass_w8a8_weight_scale.cpu().numpy().ravel(), rs)
     assert m._cutlass_w8a8_stream_loaded is True and m._cutlass_w8a8_stream_load_pending is False
 
@@ -141,11 +146,14 @@ def test_model_level_int8_flow(oracle, device):
     assert receipt["linear_count"] == 4 and receipt["post_load_conversion_linear_count"] == 0
     assert receipt["quantized_weight_bytes"] * 2 == receipt["source_weight_bytes"]
     assert w8a8.enable_h3_cutlass_w8a8_workspace_(model)["linear_count"] == 4
-    x = activations(2 * 96, 256, seed=12, outlier_channels=2)
-    for name in ("blocks.2.attn.qkv_proj", "blocks.3.mlp.fc1"):
-        out = model.get_submodule(name)(x.reshape(2, 96, 256).to(device))
-        torch.cuda.synchronize()
-        np.testing.assert_array_equal(bits16(out).reshape(192, -1), _int8_reference(oracle, x, sources[name]))
+    assert all(getattr(model.get_submodule(n).weight, "_h3q_tiled", False) for n in names["quantized_linear_names"])
+    for tokens in (2 * 96, 2 * 40, 7):   # large GEMM, then the weight-streaming GEMM (tiled activations)
+        x = activations(tokens, 256, seed=12 + tokens, outlier_channels=2)
+        for name in ("blocks.2.attn.qkv_proj", "blocks.3.mlp.fc1"):
+            out = model.get_submodule(name)(x.reshape(1, tokens, 256).to(device))
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(bits16(out).reshape(tokens, -1),
+                                          _int8_reference(oracle, x, sources[name]))
 
 
 def test_fp8_tensor_quantizers(oracle, device):
@@ -178,15 +186,17 @@ def test_fp8_w8a8_module_dispatch(oracle, device):
     # fc2 of block 2 stays bf16 and runs F.linear
     fc2 = model.get_submodule("blocks.2.mlp.fc2")
     assert fc2.weight.dtype == torch.bfloat16
-    xs = activations(150, 256, seed=7, outlier_channels=3)
     fc1 = model.get_submodule("blocks.2.mlp.fc1")
-    out = fc1(xs.reshape(3, 50, 256).to(device))
-    torch.cuda.synchronize()
-    assert tuple(out.shape) == (3, 50, 512)
-    rqa, rsa = oracle.quant_rows(bits16(xs), "e4m3")
+    assert getattr(fc1.weight, "_h3q_tiled", False)
     rqw, rsw = oracle.quant_rows(bits16(originals["blocks.2.mlp.fc1"]), "e4m3")
-    np.testing.assert_array_equal(bits8(fc1.weight), rqw)
-    _assert_fp8_close(oracle, bits16(out).reshape(150, 512), rqa, rsa, rqw, rsw, None)
+    np.testing.assert_array_equal(bits8(fc1.weight), to_tiled(rqw))
+    for tokens in (150, 48):   # large GEMM, then the weight-streaming GEMM
+        xs = activations(tokens, 256, seed=7 + tokens, outlier_channels=3)
+        out = fc1(xs.reshape(1, tokens, 256).to(device))
+        torch.cuda.synchronize()
+        assert tuple(out.shape) == (1, tokens, 512)
+        rqa, rsa = oracle.quant_rows(bits16(xs), "e4m3")
+        _assert_fp8_close(oracle, bits16(out).reshape(tokens, 512), rqa, rsa, rqw, rsw, None)
 
 
 def test_fp8_per_tensor_module_dispatch(oracle, device):

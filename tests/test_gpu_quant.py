@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import activations, bits8, bits16, from_bits16
+from _util import activations, bits8, bits16, from_bits16, weights
 
 pytestmark = pytest.mark.gpu
 
@@ -133,3 +133,25 @@ def test_full_size_activations(ops, oracle, device, name, m, k, fmt, rounding, s
     print(f"full-size act quant {name}", flush=True)
     x = activations(m, k, seed=0, outlier_channels=max(1, k // 100), outlier_scale=15.0, student_t=student)
     _check_rows(ops, oracle, x, device, fmt, rounding)
+
+
+@pytest.mark.parametrize("fmt,rounding", [("e4m3", "div"), ("int8", "div"), ("int8", "rcp")])
+@pytest.mark.parametrize("n,k,chunk", [(64, 512, 64), (96, 1024, 40), (48, 5120, 7), (16, 128, 16)])
+def test_tiled_quantizer_matches_permuted_oracle(ops, oracle, device, fmt, rounding, n, k, chunk):
+    """h3q_quant_rows_tiled in row chunks (any chunk size, like the streamed
+    loader) == the oracle's row-major codes permuted into the tiled layout."""
+    from _util import to_tiled
+
+    w = weights(n, k, seed=n + k)
+    f = ops.FMT_E4M3FN if fmt == "e4m3" else ops.FMT_INT8
+    r = ops.ROUND_DIV if rounding == "div" else ops.ROUND_RCP_MUL
+    codes = torch.zeros((n, k), device=device, dtype=ops.code_dtype(f))
+    scales = torch.empty((n, 1), device=device, dtype=torch.float32)
+    wg = w.to(device)
+    for r0 in range(0, n, chunk):
+        r1 = min(n, r0 + chunk)
+        ops.quant_rows_tiled(wg[r0:r1], f, r, codes=codes, row0=r0, scales=scales[r0:r1])
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_rows(bits16(w), fmt, rounding)
+    np.testing.assert_array_equal(bits8(codes), to_tiled(rq.view(np.uint8)))
+    np.testing.assert_array_equal(scales.cpu().numpy().ravel(), rs)
