@@ -4,22 +4,32 @@ One step is one pass of the quantized-linear hot path over one batch of the
 c2 workload (DiT QKV projection at a 480p streaming chunk):
 
     X [8192, 5120] bf16  --per-token dynamic e4m3fn act quant-->  codes + scales
-    codes x W [15360, 5120] e4m3fn (per-channel scales, quantized offline)
-      + bias bf16  --scaled MFMA GEMM, fused dequant + bias-->  Y [8192, 15360] bf16
+    codes x W [15360, 5120] e4m3fn (per-channel scales, quantized offline into
+      the tiled weight layout) + bias bf16  --scaled MFMA GEMM, fused dequant
+      + bias-->  Y [8192, 15360] bf16
 
 Inputs are synthetic (seed 0, 1% outlier channels x15) and resident in HBM
 before the timed region; four activation buffers rotate so the act-quant
-reads exceed the 256 MB Infinity Cache.  `value` is 2*M*N*K / step time.
-Each kernel is also timed alone with HIP events on the stream it runs on
-(torch's current stream) over the timed steps: the GEMM gives `roofline`
-(MFMA-bound, FP8 dense peak 5.0 PFLOP/s) and the act-quant its HBM GB/s
-(3*M*K + 4*M bytes per call against 8 TB/s).  `cpu_baseline` times the
-reference's own torch expressions (oracle/torch_path.py) on the host cores
-over one full c2 batch, repeated for about 12 s of CPU work.  `traffic` is
-read from profiles/gemm_fp8_c2_traffic.json (rocprof FETCH_SIZE/WRITE_SIZE
-of this same command, scaled by a known-size copy).
+reads exceed the 256 MB Infinity Cache.  ``value`` is 2*M*N*K / step time.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+Each kernel is also timed with HIP events on the stream it runs on (torch's
+current stream): the GEMM over the timed steps gives ``roofline`` (MFMA-bound,
+FP8 dense peak 5.0 PFLOP/s); the act-quant, timed back to back over the
+rotating inputs, gives ``act_quant`` (HBM-bound: 3*M*K + 4*M bytes per call
+against 8 TB/s; its time inside the step, right after the previous GEMM's
+252 MB of output, is reported beside it).  ``traffic`` is read from
+profiles/gemm_fp8_c2_traffic.json (rocprofv3 FETCH_SIZE / WRITE_SIZE of this
+same command, scaled by a copy of known size) when it belongs to the GEMM
+kernel measured here.
+
+The other BASELINE configurations are timed as secondary objects (not the
+headline): ``c3`` FFN up / down at 768p with the rank-128 LoRA epilogue, ``c4``
+skinny M in {16, 64, 128} (weight-streaming, HBM roofline; launches replayed
+from a HIP graph, weights rotated past the Infinity Cache) and ``c5`` the int8
+W8A8 GEMM at 1080p.  ``cpu_baseline`` times the reference's own torch
+expressions (oracle/torch_path.py) on the host cores over one full c2 batch.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu-baseline]
 """
 
 from __future__ import annotations
@@ -35,26 +45,161 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 FP8_PEAK_TFLOPS = 5000.0   # MI355X dense FP8 MFMA
+INT8_PEAK_TOPS = 5000.0    # MI355X dense INT8 MFMA
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 M, K, N = 8192, 5120, 15360
 TRAFFIC_FILE = ROOT / "profiles" / "gemm_fp8_c2_traffic.json"
+GEMM_KERNEL_TAG = "Tile<256, 256, 128, 2, 4, 4, 4>, 0, 0, false, true, true, true"
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def gpu_randn(torch, shape, gen, device, scale=1.0):
+    return (torch.randn(shape, generator=gen, device=device) * scale).to(torch.bfloat16)
+
+
 def make_inputs(torch, device, rotations: int):
-    gen = torch.Generator().manual_seed(0)
+    gen = torch.Generator(device=device).manual_seed(0)
     xs = []
-    for r in range(rotations):
-        x = torch.randn(M, K, generator=gen)
-        idx = torch.randperm(K, generator=gen)[: K // 100]
+    for _ in range(rotations):
+        x = torch.randn(M, K, generator=gen, device=device)
+        idx = torch.randperm(K, generator=gen, device=device)[: K // 100]
         x[:, idx] *= 15.0
-        xs.append(x.to(torch.bfloat16).to(device))
-    w = (torch.randn(N, K, generator=gen) * 0.02).to(torch.bfloat16)
-    bias = (torch.randn(N, generator=gen) * 0.01).to(torch.bfloat16)
+        xs.append(x.to(torch.bfloat16))
+    w = gpu_randn(torch, (N, K), gen, device, 0.02)
+    bias = gpu_randn(torch, (N,), gen, device, 0.01)
     return xs, w, bias
+
+
+def time_events(torch, fn, iters: int) -> float:
+    """Average ms of fn() over iters launches, HIP events on the current stream."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(iters):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def bench_c3(torch, ops, dev) -> dict:
+    """FFN at 768p, M=24576, up N=13824 K=5120 and down
+    N=5120 K=13824, e4m3 per-token x per-channel, rank-128 LoRA (scale 1.0)
+    added in the GEMM epilogue.  Times act-quant + LoRA down + scaled GEMM."""
+    gen = torch.Generator(device=dev).manual_seed(0)
+    m, out = 24576, {}
+    for name, n, k in (("up", 13824, 5120), ("down", 5120, 13824)):
+        x = gpu_randn(torch, (m, k), gen, dev)
+        qw, sw = ops.quant_rows_tiled(gpu_randn(torch, (n, k), gen, dev, 0.02), ops.FMT_E4M3FN)
+        la, lb = gpu_randn(torch, (128, k), gen, dev, 0.01), gpu_randn(torch, (n, 128), gen, dev, 0.01)
+        q_a = torch.empty(m, k, device=dev, dtype=torch.float8_e4m3fn)
+        s_a = torch.empty(m, 1, device=dev, dtype=torch.float32)
+        t = torch.empty(m, 128, device=dev, dtype=torch.bfloat16)
+        y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+
+        def quant(_i):
+            ops.quant_rows(x, ops.FMT_E4M3FN, codes=q_a, scales=s_a)
+            ops.lora_down(x, la, out=t)
+
+        def gemm(_i):
+            ops.scaled_mm(q_a, qw, s_a.reshape(-1), sw.reshape(-1), lora_t=t, lora_b=lb, lora_scale=1.0, out=y,
+                          b_tiled=True)
+
+        for f in (quant, gemm):
+            f(0)
+        torch.cuda.synchronize()
+        q_ms = time_events(torch, quant, 5)
+        g_ms = time_events(torch, gemm, 5)
+        fl = 2.0 * m * n * k
+        out[name] = {"M": m, "N": n, "K": k, "gemm_us": round(g_ms * 1e3, 1),
+                     "gemm_fp8_tflops": round(fl / (g_ms * 1e-3) / 1e12, 1),
+                     "pct_fp8_peak": round(100 * fl / (g_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 1),
+                     "act_quant_plus_lora_down_us": round(q_ms * 1e3, 1),
+                     "step_tflops": round(fl / ((g_ms + q_ms) * 1e-3) / 1e12, 1),
+                     "lora_gflop": round(2.0 * m * 128 * (k + n) / 1e9, 1)}
+        del x, qw, sw, la, lb, q_a, s_a, t, y
+    return out
+
+
+def bench_c4(torch, ops, dev) -> dict:
+    """skinny M in {16, 64, 128}, K = N = 5120, tiled
+    e4m3 weights, activations quantized into the tiled layout.  Bytes per call
+    N*K + 4N + M*K + 4M + 2MN against 8 TB/s; twelve weight copies (315 MB)
+    rotate past the Infinity Cache; 48 launches captured in a HIP graph."""
+    gen = torch.Generator(device=dev).manual_seed(0)
+    n = k = 5120
+    copies = 12
+    ws = []
+    for _ in range(copies):
+        qw, sw = ops.quant_rows_tiled(gpu_randn(torch, (n, k), gen, dev, 0.02), ops.FMT_E4M3FN)
+        ws.append((qw, sw.reshape(-1)))
+    res = {}
+    for m in (16, 64, 128):
+        x = gpu_randn(torch, (m, k), gen, dev)
+        q_a, s_a = ops.quant_rows_tiled(x, ops.FMT_E4M3FN)
+        s_a = s_a.reshape(-1)
+        y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        per = 48
+
+        def launches():
+            for i in range(per):
+                qw, sw = ws[i % copies]
+                ops.scaled_mm(q_a, qw, s_a, sw, out=y, a_tiled=True, b_tiled=True, m=m)
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            launches()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            launches()
+        graph.replay()
+        torch.cuda.synchronize()
+        ms = time_events(torch, lambda _i: graph.replay(), 5) / per
+        byts = n * k + 4 * n + m * k + 4 * m + 2 * m * n
+        gbs = byts / (ms * 1e-3) / 1e9
+        res[f"M{m}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3),
+                        "bytes": byts}
+    return res
+
+
+def bench_c5(torch, ops, dev) -> dict:
+    """int8 W8A8 at 1080p, M=40960, K=N=5120: per-token
+    int8 act quant (vLLM formula) + int32-exact GEMM with fused dequant."""
+    gen = torch.Generator(device=dev).manual_seed(0)
+    m, n, k = 40960, 5120, 5120
+    x = torch.randn(m, k, generator=gen, device=dev)
+    idx = torch.randperm(k, generator=gen, device=dev)[: k // 100]
+    chi = torch.distributions.Chi2(torch.full((idx.numel(),), 3.0, device=dev)).sample((m,))
+    x[:, idx] = torch.randn(m, idx.numel(), generator=gen, device=dev) / torch.sqrt(chi / 3.0)
+    x = x.to(torch.bfloat16)
+    qw, sw = ops.quant_rows_tiled(gpu_randn(torch, (n, k), gen, dev, 0.02), ops.FMT_INT8)
+    q_a = torch.empty(m, k, device=dev, dtype=torch.int8)
+    s_a = torch.empty(m, 1, device=dev, dtype=torch.float32)
+    y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+
+    def quant(_i):
+        ops.quant_rows(x, ops.FMT_INT8, ops.ROUND_RCP_MUL, codes=q_a, scales=s_a)
+
+    def gemm(_i):
+        ops.scaled_mm(q_a, qw, s_a.reshape(-1), sw.reshape(-1), out=y, b_tiled=True)
+
+    quant(0)
+    gemm(0)
+    torch.cuda.synchronize()
+    q_ms = time_events(torch, quant, 5)
+    g_ms = time_events(torch, gemm, 5)
+    ops_ = 2.0 * m * n * k
+    q_bytes = 3 * m * k + 4 * m
+    return {"M": m, "N": n, "K": k, "gemm_us": round(g_ms * 1e3, 1),
+            "gemm_int8_tops": round(ops_ / (g_ms * 1e-3) / 1e12, 1),
+            "pct_int8_peak": round(100 * ops_ / (g_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 1),
+            "act_quant_us": round(q_ms * 1e3, 1), "act_quant_GB/s": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
+            "step_tops": round(ops_ / ((g_ms + q_ms) * 1e-3) / 1e12, 1)}
 
 
 def cpu_baseline(torch, w_cpu, bias_cpu, x_cpu, budget_s: float = 12.0) -> dict:
@@ -92,6 +237,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the c3 / c4 / c5 secondary measurements")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 512 MiB device copy (known bytes) for scaling rocprof "
                          "FETCH_SIZE / WRITE_SIZE counters")
@@ -110,23 +256,26 @@ def main() -> int:
     dev = torch.device("cuda:0")
     rotations = 4
     xs, w, bias = make_inputs(torch, dev, rotations)
-    x_cpu = xs[0].cpu()
-    w_dev, bias_dev = w.to(dev), bias.to(dev)
-    q_w, s_w = ops.quant_rows(w_dev, ops.FMT_E4M3FN)       # offline weight quantization
+    q_w, s_w = ops.quant_rows_tiled(w, ops.FMT_E4M3FN)      # offline weight quantize + pack
     s_w = s_w.reshape(-1)
     q_a = torch.empty(M, K, device=dev, dtype=torch.float8_e4m3fn)
     s_a = torch.empty(M, 1, device=dev, dtype=torch.float32)
     out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
     torch.cuda.synchronize()
 
+    def quant(i: int):
+        ops.quant_rows(xs[i % rotations], ops.FMT_E4M3FN, codes=q_a, scales=s_a)
+
+    def gemm(_i: int):
+        ops.scaled_mm(q_a, q_w, s_a.reshape(-1), s_w, bias=bias, out=out, b_tiled=True)
+
     def step(i: int, ev=None):
-        x = xs[i % rotations]
         if ev is not None:
             ev[0].record()
-        ops.quant_rows(x, ops.FMT_E4M3FN, codes=q_a, scales=s_a)
+        quant(i)
         if ev is not None:
             ev[1].record()
-        ops.scaled_mm(q_a, q_w, s_a.reshape(-1), s_w, bias=bias_dev, out=out)
+        gemm(i)
         if ev is not None:
             ev[2].record()
 
@@ -146,8 +295,9 @@ def main() -> int:
     for i in range(args.steps):
         step(i, evs[i])
     torch.cuda.synchronize()
-    q_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    q_step_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
     g_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    q_ms = time_events(torch, quant, 4 * rotations)        # act-quant back to back, rotating inputs
 
     flops = 2.0 * M * N * K
     ms_per_step = elapsed / args.steps * 1e3
@@ -159,7 +309,9 @@ def main() -> int:
     traffic = None
     if TRAFFIC_FILE.exists():
         try:
-            traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+            rec = json.loads(TRAFFIC_FILE.read_text())
+            if GEMM_KERNEL_TAG in rec.get("kernel", ""):
+                traffic = rec.get("hbm_bytes_per_launch")
         except (ValueError, OSError):
             traffic = None
 
@@ -180,7 +332,7 @@ def main() -> int:
             "workload": "c2: DiT QKV projection, 480p streaming chunk (BASELINE configs[1])",
             "M_tokens": M, "K": K, "N": N,
             "act_quant": "per-token dynamic e4m3fn",
-            "weight_quant": "per-output-channel e4m3fn (offline)",
+            "weight_quant": "per-output-channel e4m3fn (offline, tiled layout)",
             "bias": True, "out": "bf16",
             "activation_buffers_rotated": rotations,
         },
@@ -194,6 +346,7 @@ def main() -> int:
             "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
             "traffic": traffic,
             "avg_launch_us": round(g_ms * 1e3, 2),
+            "algorithmic_flops": flops,
         },
         "act_quant": {
             "kernel": "h3q quant_rows_vec_kernel (per-token e4m3fn)",
@@ -203,6 +356,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(q_gbs / HBM_PEAK_GBS, 4),
             "avg_launch_us": round(q_ms * 1e3, 2),
+            "in_step_us": round(q_step_ms * 1e3, 2),
             "algorithmic_bytes": q_bytes,
         },
     }
@@ -214,8 +368,19 @@ def main() -> int:
         torch.cuda.synchronize()
         result["calibration_copy_bytes"] = int(src.numel() * src.element_size())
         del src, dst
+    x_cpu, w_cpu, bias_cpu = xs[0].cpu(), w.cpu(), bias.cpu()
+    del xs, w, q_w, q_a, out
+    torch.cuda.empty_cache()
+    if not args.no_extra:
+        log("secondary configs: c3, c4, c5")
+        result["c3"] = bench_c3(torch, ops, dev)
+        torch.cuda.empty_cache()
+        result["c4"] = bench_c4(torch, ops, dev)
+        torch.cuda.empty_cache()
+        result["c5"] = bench_c5(torch, ops, dev)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(torch, w, bias, x_cpu)
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(torch, w_cpu, bias_cpu, x_cpu)
     print(json.dumps(result), flush=True)
     return 0
 

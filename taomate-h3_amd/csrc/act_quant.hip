@@ -97,39 +97,42 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(const uint16_t* __r
                                                              int64_t ldq, int64_t row0,
                                                              float* __restrict__ scales) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
     const int nvec = k >> 3;
-    uint4 v[NV];
-    uint32_t m = 0;
+    // Rows are dealt to waves in order (row = wave id + i * waves in the grid),
+    // so the rows in flight at any moment form one contiguous band of X.
+    const int64_t step = (int64_t)gridDim.x * 4;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += step) {
+        const uint4* xr = reinterpret_cast<const uint4*>(x + row * ldx);
+        uint4 v[NV];
+        uint32_t m = 0;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int vec = i * 64 + lane;
-        if (vec < nvec) {
-            v[i] = xr[vec];
-        } else {
-            v[i] = make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < NV; ++i) {
+            const int vec = i * 64 + lane;
+            if (vec < nvec) {
+                v[i] = xr[vec];
+            } else {
+                v[i] = make_uint4(0, 0, 0, 0);
+            }
+            m = pk_abs_max(m, v[i].x);
+            m = pk_abs_max(m, v[i].y);
+            m = pk_abs_max(m, v[i].z);
+            m = pk_abs_max(m, v[i].w);
         }
-        m = pk_abs_max(m, v[i].x);
-        m = pk_abs_max(m, v[i].y);
-        m = pk_abs_max(m, v[i].z);
-        m = pk_abs_max(m, v[i].w);
-    }
-    const float amax = wave_max(amax_from_packed(m));
-    RowQuant<FMT, ROUND> rq;
-    rq.init(amax);
+        const float amax = wave_max(amax_from_packed(m));
+        RowQuant<FMT, ROUND> rq;
+        rq.init(amax);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int vec = i * 64 + lane;
-        if (vec < nvec) {
-            uint2 out;
-            out.x = rq.pack4(v[i].x, v[i].y);
-            out.y = rq.pack4(v[i].z, v[i].w);
-            *reinterpret_cast<uint2*>(q + code_offset<TILED>(row0 + row, 8 * (int64_t)vec, ldq)) = out;
+        for (int i = 0; i < NV; ++i) {
+            const int vec = i * 64 + lane;
+            if (vec < nvec) {
+                uint2 out;
+                out.x = rq.pack4(v[i].x, v[i].y);
+                out.y = rq.pack4(v[i].z, v[i].w);
+                *reinterpret_cast<uint2*>(q + code_offset<TILED>(row0 + row, 8 * (int64_t)vec, ldq)) = out;
+            }
         }
+        if (lane == 0) scales[row] = rq.s;
     }
-    if (lane == 0) scales[row] = rq.s;
 }
 
 // General path (any K, any alignment): one workgroup per row, two passes.
@@ -156,10 +159,14 @@ __global__ __launch_bounds__(256) void quant_rows_any_kernel(const uint16_t* __r
     if (threadIdx.x == 0) scales[row] = rq.s;
 }
 
+constexpr int64_t kRowBlocks = 1024;
+
 template <int FMT, int ROUND, int NV, bool TILED>
 static hipError_t launch_rows_vec(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, uint8_t* q,
                                   int64_t ldq, int64_t row0, float* scales, hipStream_t st) {
-    const int64_t blocks = (rows + 3) / 4;
+    // One wave per row up to 4 waves per SIMD of the chip (1024 workgroups of
+    // four waves on 256 CUs); beyond that each wave takes several rows.
+    const int64_t blocks = (rows + 3) / 4 < kRowBlocks ? (rows + 3) / 4 : kRowBlocks;
     hipLaunchKernelGGL((quant_rows_vec_kernel<FMT, ROUND, NV, TILED>), dim3((unsigned)blocks), dim3(256), 0, st, x,
                        ldx, rows, (int)k, q, ldq, row0, scales);
     return hipGetLastError();
@@ -174,10 +181,15 @@ static hipError_t dispatch_rows(const uint16_t* x, int64_t ldx, int64_t rows, in
     if (aligned) {
         if (nv <= 2) return launch_rows_vec<FMT, ROUND, 2, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
         if (nv <= 4) return launch_rows_vec<FMT, ROUND, 4, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+        // nv = 16-byte vectors per lane (512 columns each); exact sizes for the H3
+        // and benchmark widths (K = 5120, 5376, 7168, 13824) keep no idle vectors.
         if (nv <= 8) return launch_rows_vec<FMT, ROUND, 8, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
-        if (nv <= 12) return launch_rows_vec<FMT, ROUND, 12, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+        if (nv <= 10) return launch_rows_vec<FMT, ROUND, 10, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+        if (nv <= 11) return launch_rows_vec<FMT, ROUND, 11, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+        if (nv <= 14) return launch_rows_vec<FMT, ROUND, 14, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
         if (nv <= 16) return launch_rows_vec<FMT, ROUND, 16, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
         if (nv <= 24) return launch_rows_vec<FMT, ROUND, 24, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
+        if (nv <= 28) return launch_rows_vec<FMT, ROUND, 28, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
         if (nv <= 32) return launch_rows_vec<FMT, ROUND, 32, TILED>(x, ldx, rows, k, q, ldq, row0, scales, st);
     }
     hipLaunchKernelGGL((quant_rows_any_kernel<FMT, ROUND, TILED>), dim3((unsigned)rows), dim3(256), 0, st, x, ldx,
