@@ -200,14 +200,15 @@ __device__ __forceinline__ void mma_stage(const H3Q_LDS uint8_t* sa, const H3Q_L
     }
 }
 
-// Logical tile for this workgroup.  Workgroups are dealt to the 8 XCDs round
+// Logical tile of block index bid.  Workgroups are dealt to the 8 XCDs round
 // robin (XCD = blockIdx % 8); give each XCD a contiguous run of tiles so the
 // tiles resident on one XCD share A and B rows in that XCD's L2.  Within the
-// run, tiles go column-major in groups of kGroupM tile-rows.
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+// run, tiles go column-major in groups of kGroupM tile-rows.  A persistent
+// grid passes bid = blockIdx + j * gridDim with gridDim % 8 == 0, which keeps
+// bid % 8 equal to the XCD the workgroup runs on.
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
     constexpr int kXcds = 8, kGroupM = 8;
     const int total = tiles_m * tiles_n;
-    const int bid = blockIdx.x;
     const int q = total / kXcds, rem = total % kXcds;
     const int xcd = bid % kXcds, local = bid / kXcds;
     const int t = xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 5, c32 = lane & 31;
     int tm, tn;
-    tile_coords(tiles_m, tiles_n, tm, tn);
+    tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const int wm0 = (wave / T::WAVES_N) * T::WM, wn0 = (wave % T::WAVES_N) * T::WN;
 
@@ -426,6 +427,185 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
     }
 }
 
+// Lane index that the compiler cannot hoist out of a loop: recomputing
+// lane-derived offsets inside each tile iteration keeps them from staying
+// live (in registers) across the epilogue of the persistent kernel.
+__device__ __forceinline__ int opaque_lane() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
+// Persistent scaled GEMM (e4m3 / int8 -> bf16, optional bias, no LoRA, 4-column
+// stores).  A grid of at most one workgroup per CU walks the output tiles
+// blockIdx.x, blockIdx.x + gridDim.x, ... with one continuous 2-stage copy
+// ring: the last k-tile of a tile issues the first stage of the next one, so
+// that copy is in flight during the last MFMAs and the epilogue, and no
+// workgroup is relaunched between tiles (on MI355X a 16-wave workgroup with
+// 128 KiB of LDS takes about 7 us from the end of one to the start of the next
+// on the same CU, measured with s_memrealtime).  The tile's per-row /
+// per-column scales and bias are copied into LDS with its first stage,
+// double-buffered by tile parity; a per-tensor scale is read once.
+// Arithmetic, k order and rounding are those of gemm_kernel: both produce the
+// same bits.
+template <class T, int OP, bool BIAS, bool TB>
+__global__ __launch_bounds__(T::NT, T::OCC) void gemm_persistent_kernel(GemmArgs p, int tiles_m, int tiles_n) {
+    constexpr int BM = T::BM, BN = T::BN, BK = T::BK, TM = T::TM, TN = T::TN;
+    static_assert(BM == 256 && BN == 256, "one 1 KiB copy per scale vector");
+    static_assert(T::STAGES == 2, "two-stage ring");
+    static_assert(OP != kOpBF16, "codes only");
+    using acc_t = typename Mfma<OP>::acc_t;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_ring[2 * T::STAGE_BYTES];
+    // Per tile parity: row scales [BM] f32 | column scales [BN] f32 | bias [BN] bf16.
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_ep[2 * 3 * 1024];
+    H3Q_LDS uint8_t* const lds = (H3Q_LDS uint8_t*)lds_ring;
+    H3Q_LDS uint8_t* const ep = (H3Q_LDS uint8_t*)lds_ep;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm0 = (wave / T::WAVES_N) * T::WM, wn0 = (wave % T::WAVES_N) * T::WN;
+    const int ktiles = (int)((p.k + BK - 1) / BK);
+    const int ntiles = (tiles_m * tiles_n - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const bool row_scales = p.a_scale_per_row != 0, col_scales = p.b_scale_per_col != 0;
+    // A per-tensor scale fills its LDS vector (both parities) once; per-row /
+    // per-column vectors are copied per tile.
+    if (!row_scales || !col_scales) {
+        const float sa0 = row_scales ? 0.0f : p.a_scale[0], sw0 = col_scales ? 0.0f : p.b_scale[0];
+        for (int c = threadIdx.x; c < 2 * 256; c += T::NT) {
+            H3Q_LDS float* e = (H3Q_LDS float*)(ep + (c >> 8) * 3072);
+            if (!row_scales) e[c & 255] = sa0;
+            if (!col_scales) e[256 + (c & 255)] = sw0;
+        }
+    }
+
+    // Origin and extent of local tile j.
+    struct TileSrc {
+        int m0, n0, rows, cols;
+    };
+    auto tile_src = [&](int j) {
+        int tm, tn;
+        tile_coords((int)blockIdx.x + j * (int)gridDim.x, tiles_m, tiles_n, tm, tn);
+        TileSrc t;
+        t.m0 = tm * BM;
+        t.n0 = tn * BN;
+        t.rows = (int)(p.m - t.m0 < BM ? p.m - t.m0 : BM);
+        t.cols = (int)(p.n - t.n0 < BN ? p.n - t.n0 : BN);
+        return t;
+    };
+    const int64_t steps = p.k / 128;  // tiled B: 128-byte k-steps
+    auto a_src = [&](const TileSrc& t) {
+        return CopySrc((const uint8_t*)p.a + (int64_t)t.m0 * p.lda, (uint32_t)((int64_t)t.rows * p.lda));
+    };
+    auto b_src = [&](const TileSrc& t) {
+        if constexpr (TB)
+            return CopySrc((const uint8_t*)p.b + (int64_t)(t.n0 / 16) * steps * 2048,
+                           (uint32_t)((t.cols + 15) / 16 * steps * 2048));
+        else
+            return CopySrc((const uint8_t*)p.b + (int64_t)t.n0 * p.ldb, (uint32_t)((int64_t)t.cols * p.ldb));
+    };
+    // The epilogue vectors of tile j, issued ahead of its first stage so the
+    // wait for that stage covers them.  Past the operand ends copies read zeros.
+    auto issue_vectors = [&](const TileSrc& t, int j, int ln) {
+        H3Q_LDS uint8_t* e = ep + (j & 1) * 3072;
+        if (wave == 0 && row_scales)
+            copy16(CopySrc(p.a_scale + t.m0, (uint32_t)t.rows * 4u), (uint32_t)(uintptr_t)e, 16u * ln);
+        if (wave == 1 && col_scales)
+            copy16(CopySrc(p.b_scale + t.n0, (uint32_t)t.cols * 4u), (uint32_t)(uintptr_t)(e + 1024), 16u * ln);
+        if (BIAS && wave == 2)
+            copy16(CopySrc(p.bias + t.n0, (uint32_t)t.cols * 2u), (uint32_t)(uintptr_t)(e + 2048),
+                   ln < 32 ? 16u * ln : 0x80000000u);
+    };
+    auto issue_stage = [&](const CopySrc& ra, const CopySrc& rb, int nblk, int kt, int buf, int ln) {
+        H3Q_LDS uint8_t* dst = lds + buf * T::STAGE_BYTES;
+        load_tile<T, BM>(ra, dst, (uint32_t)p.lda, (int64_t)kt * BK, p.k, wave, ln);
+        if constexpr (TB) load_tile_tiled<T, BN>(rb, dst + BM * BK, steps, kt, nblk, wave, ln);
+        else load_tile<T, BN>(rb, dst + BM * BK, (uint32_t)p.ldb, (int64_t)kt * BK, p.k, wave, ln);
+    };
+
+    {
+        const TileSrc t = tile_src(0);
+        issue_vectors(t, 0, lane);
+        issue_stage(a_src(t), b_src(t), (t.cols + 15) / 16, 0, 0, lane);
+    }
+    int rd = 0;
+    for (int j = 0; j < ntiles; ++j) {
+        const int lane = opaque_lane();
+        CopySrc ra(nullptr, 0), rb(nullptr, 0);
+        int nblk;
+        {
+            const TileSrc t = tile_src(j);
+            ra = a_src(t);
+            rb = b_src(t);
+            nblk = (t.cols + 15) / 16;
+        }
+        acc_t acc[TM][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int jj = 0; jj < TN; ++jj) acc[i][jj] = acc_t{};
+        for (int kt = 0; kt < ktiles; ++kt) {
+            // Everything this wave issued has landed (the copies of this
+            // stage, and the previous epilogue's stores); the barrier makes
+            // every wave's copies visible and frees the other buffer.
+            wait_vmcnt<0>();
+            ring_barrier();
+            if (kt + 1 < ktiles) {
+                issue_stage(ra, rb, nblk, kt + 1, rd ^ 1, lane);
+            } else if (j + 1 < ntiles) {
+                const TileSrc t = tile_src(j + 1);
+                issue_vectors(t, j + 1, lane);
+                issue_stage(a_src(t), b_src(t), (t.cols + 15) / 16, 0, rd ^ 1, lane);
+            }
+            const H3Q_LDS uint8_t* st = lds + rd * T::STAGE_BYTES;
+            mma_stage<T, OP, TB>(st, st + BM * BK, wm0, wn0, lane, acc);
+            rd ^= 1;
+        }
+
+        // Epilogue: v = s_a[m] * (s_w[n] * float(acc)) [fma with bias[n]] ->
+        // bf16, 4 columns per 8-byte store through a buffer resource over the
+        // tile's rows (rows past M are dropped by the hardware; a column
+        // group past N gets an out-of-range offset).
+        {
+            const TileSrc cur = tile_src(j);
+            const int g = lane >> 5, c32 = lane & 31;
+            const H3Q_LDS uint8_t* e = ep + (j & 1) * 3072;
+            const H3Q_LDS float* sa_l = (const H3Q_LDS float*)e;
+            const H3Q_LDS float* sw_l = (const H3Q_LDS float*)(e + 1024);
+            const H3Q_LDS uint16_t* bias_l = (const H3Q_LDS uint16_t*)(e + 2048);
+            const __amdgpu_buffer_rsrc_t ro =
+                make_rsrc((uint8_t*)p.out + (int64_t)cur.m0 * p.ldo * 2, (uint32_t)((int64_t)cur.rows * p.ldo * 2));
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int ml = wm0 + 32 * i + c32;
+                const float sa = sa_l[ml];
+                const uint32_t row_off = (uint32_t)ml * (uint32_t)p.ldo * 2u;
+#pragma unroll
+                for (int jj = 0; jj < TN; ++jj) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int nl = wn0 + 32 * jj + 8 * q + 4 * g;
+                        const v4f sw4 = *(const H3Q_LDS v4f*)(sw_l + nl);
+                        float y[4];
+                        if constexpr (BIAS) {
+                            const v2u b4 = *(const H3Q_LDS v2u*)(bias_l + nl);
+                            const float bias[4] = {bf16_lo(b4[0]), bf16_hi(b4[0]), bf16_lo(b4[1]), bf16_hi(b4[1])};
+#pragma unroll
+                            for (int x = 0; x < 4; ++x)
+                                y[x] = __builtin_fmaf(sa, __fmul_rn(sw4[x], (float)acc[i][jj][4 * q + x]), bias[x]);
+                        } else {
+#pragma unroll
+                            for (int x = 0; x < 4; ++x) y[x] = __fmul_rn(sa, __fmul_rn(sw4[x], (float)acc[i][jj][4 * q + x]));
+                        }
+                        const uint32_t off = nl < cur.cols ? row_off + (uint32_t)(cur.n0 + nl) * 2u : 0xFFFFFFF0u;
+                        __builtin_amdgcn_raw_buffer_store_b64(v2u{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])},
+                                                              ro, off, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+}
+
 template <class T, int OP, int EPI, bool LORA, bool VEC, bool BIAS>
 hipError_t launch_tile(const GemmArgs& a, hipStream_t st) {
     const int tiles_m = (int)((a.m + T::BM - 1) / T::BM), tiles_n = (int)((a.n + T::BN - 1) / T::BN);
@@ -442,9 +622,41 @@ hipError_t launch_tile(const GemmArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// Selects the epilogue variant for a scaled GEMM.
+// Workgroups of the persistent GEMM: one per CU of the current device (the
+// LDS ring allows one per CU), rounded down to a multiple of the 8 XCDs.
+static int persistent_grid(int tiles) {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    int cus = dev < 64 ? __atomic_load_n(&cached[dev], __ATOMIC_RELAXED) : 0;
+    if (cus == 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8) cus = 8;
+        if (dev < 64) __atomic_store_n(&cached[dev], cus, __ATOMIC_RELAXED);
+    }
+    cus -= cus % 8;
+    return tiles < cus ? tiles : cus;
+}
+
+template <class T, int OP, bool BIAS>
+hipError_t launch_persistent(const GemmArgs& a, hipStream_t st) {
+    const int tiles_m = (int)((a.m + T::BM - 1) / T::BM), tiles_n = (int)((a.n + T::BN - 1) / T::BN);
+    const dim3 grid((unsigned)persistent_grid(tiles_m * tiles_n));
+    if (a.b_tiled)
+        hipLaunchKernelGGL((gemm_persistent_kernel<T, OP, BIAS, true>), grid, dim3(T::NT), 0, st, a, tiles_m, tiles_n);
+    else
+        hipLaunchKernelGGL((gemm_persistent_kernel<T, OP, BIAS, false>), grid, dim3(T::NT), 0, st, a, tiles_m, tiles_n);
+    return hipGetLastError();
+}
+
+// Selects the kernel and epilogue variant for a scaled GEMM.  The persistent
+// kernel needs 4-column stores, no LoRA and at least STAGES k-tiles (its
+// epilogue vectors are double-buffered across that many stages).
 template <class T, int OP, bool LORA>
 hipError_t launch_scaled(const GemmArgs& a, hipStream_t st) {
+    if constexpr (!LORA && T::BM == 256 && T::BN == 256 && T::BK == 128) {
+        if (a.out_vec && (a.k + T::BK - 1) / T::BK >= T::STAGES)
+            return a.bias ? launch_persistent<T, OP, true>(a, st) : launch_persistent<T, OP, false>(a, st);
+    }
     if (!a.out_vec) return launch_tile<T, OP, kEpiScaled, LORA, false, false>(a, st);
     return a.bias ? launch_tile<T, OP, kEpiScaled, LORA, true, true>(a, st)
                   : launch_tile<T, OP, kEpiScaled, LORA, true, false>(a, st);
