@@ -49,7 +49,7 @@ INT8_PEAK_TOPS = 5000.0    # MI355X dense INT8 MFMA
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 M, K, N = 8192, 5120, 15360
 TRAFFIC_FILE = ROOT / "profiles" / "gemm_fp8_c2_traffic.json"
-GEMM_KERNEL_TAG = "Tile<256, 256, 128, 2, 4, 4, 4>, 0, 0, false, true, true, true"
+GEMM_KERNEL_TAG = "gemm_persistent_kernel<h3q::Tile<256, 256, 128, 2, 4, 4, 4>, 0, true, true>"
 
 
 def log(*a):
@@ -338,7 +338,7 @@ def main() -> int:
         },
         "pct_fp8_peak": round(100.0 * value / FP8_PEAK_TFLOPS, 2),
         "roofline": {
-            "kernel": "h3q gemm_kernel (scaled e4m3 GEMM + dequant + bias epilogue)",
+            "kernel": "h3q gemm_persistent_kernel (scaled e4m3 GEMM + dequant + bias epilogue)",
             "bound": "mfma",
             "achieved": round(gemm_tflops, 2),
             "peak": FP8_PEAK_TFLOPS,
