@@ -26,7 +26,8 @@ The other BASELINE configurations are timed as secondary objects (not the
 headline): ``c3`` FFN up / down at 768p with the rank-128 LoRA epilogue, ``c4``
 skinny M in {16, 64, 128} (weight-streaming, HBM roofline; launches replayed
 from a HIP graph, weights rotated past the Infinity Cache) and ``c5`` the int8
-W8A8 GEMM at 1080p.  ``cpu_baseline`` times the reference's own torch
+W8A8 GEMM at 1080p; ``f1`` the fused RMSNorm/AdaLN + int8 act-quant producer
+against the unfused pair.  ``cpu_baseline`` times the reference's own torch
 expressions (oracle/torch_path.py) on the host cores over one full c2 batch.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-extra] [--no-cpu-baseline]
@@ -164,6 +165,47 @@ def bench_c4(torch, ops, dev) -> dict:
         gbs = byts / (ms * 1e-3) / 1e9
         res[f"M{m}"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 3),
                         "bytes": byts}
+    return res
+
+
+def bench_f1(torch, ops, dev) -> dict:
+    """Next row (f)1: the QKV-input producer (RMSNorm + AdaLN modulate) with the
+    per-token int8 act-quant of the W8A8 linear fused in, against the same two
+    steps unfused (modulated bf16 rows written, then re-read by the
+    quantizer).  At the c2 activation shape and at the real H3 QKV input
+    (1088x1920 phase 0, M=6224, K=5376); four rotating inputs, four table rows.
+    Bytes: fused 2MK in + MK + 4M out; unfused adds 4MK."""
+    res = {}
+    for name, m, k in (("c2_shape", 8192, 5120), ("h3_qkv_1088p", 6224, 5376)):
+        gen = torch.Generator(device=dev).manual_seed(0)
+        xs = [gpu_randn(torch, (m, k), gen, dev) for _ in range(4)]
+        w = (1.0 + 0.1 * torch.randn(k, device=dev, generator=gen)).to(torch.bfloat16)
+        sc = gpu_randn(torch, (4, k), gen, dev, 0.1)
+        sh = gpu_randn(torch, (4, k), gen, dev, 0.1)
+        idx = torch.randint(0, 4, (m,), device=dev, generator=gen)
+        codes = torch.empty(m, k, device=dev, dtype=torch.int8)
+        scales = torch.empty(m, 1, device=dev, dtype=torch.float32)
+        y = torch.empty(m, k, device=dev, dtype=torch.bfloat16)
+
+        def fused(i):
+            ops.norm_modulate_quant(xs[i % 4], w, sc, sh, idx, 1e-6, fmt=ops.FMT_INT8, rounding=ops.ROUND_RCP_MUL,
+                                    codes=codes, scales=scales)
+
+        def unfused(i):
+            ops.norm_modulate_quant(xs[i % 4], w, sc, sh, idx, 1e-6, out=y)
+            ops.quant_rows(y, ops.FMT_INT8, ops.ROUND_RCP_MUL, codes=codes, scales=scales)
+
+        for fn in (fused, unfused):
+            for i in range(4):
+                fn(i)
+        torch.cuda.synchronize()
+        tf = time_events(torch, fused, 40) * 1e3
+        tu = time_events(torch, unfused, 40) * 1e3
+        byts = 3 * m * k + 4 * m
+        res[name] = {"M": m, "K": k, "fused_us": round(tf, 1), "unfused_us": round(tu, 1),
+                     "fused_GB/s": round(byts / tf / 1e3, 1), "frac_hbm": round(byts / tf / 1e3 / HBM_PEAK_GBS, 3),
+                     "saved_bytes": 4 * m * k}
+        del xs, codes, y
     return res
 
 
@@ -372,12 +414,14 @@ def main() -> int:
     del xs, w, q_w, q_a, out
     torch.cuda.empty_cache()
     if not args.no_extra:
-        log("secondary configs: c3, c4, c5")
+        log("secondary configs: c3, c4, c5, f1")
         result["c3"] = bench_c3(torch, ops, dev)
         torch.cuda.empty_cache()
         result["c4"] = bench_c4(torch, ops, dev)
         torch.cuda.empty_cache()
         result["c5"] = bench_c5(torch, ops, dev)
+        torch.cuda.empty_cache()
+        result["f1"] = bench_f1(torch, ops, dev)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(torch, w_cpu, bias_cpu, x_cpu)

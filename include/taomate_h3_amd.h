@@ -151,6 +151,47 @@ int h3q_gemm_i8_i32(const void* a, int64_t lda, const void* b, int64_t ldb, void
 int h3q_lora_down(const void* x, int64_t ldx, const void* lora_a, int64_t lda, void* t, int64_t ldt, int64_t m,
                   int64_t k, int64_t rank, void* stream);
 
+/*
+ * Fused RMSNorm + AdaLN modulate + per-token quantization: the producer of the
+ * QKV input of a DiT block, fused_rms_norm_modulate
+ * (H3/inference/fused_kernels.py:287-317 kernel, 700-730 wrapper), with the
+ * activation quantizer of the following W8A8 linear folded in.  For each row r
+ * (t = indices[r], a row of the [T, table_stride] scale / shift tables):
+ *   rs = 1 / sqrt(sum_k v[k]^2 / cols + eps)            (binary32; see below)
+ *   n  = bf16((v[k] * rs) * weight[k])
+ *   y  = bf16(bf16(n * bf16(1 + scale[t, k])) + shift[t, k])
+ * y goes to out (bf16, ldo elements) when out is not NULL; when codes is not
+ * NULL, y is quantized per row exactly as h3q_quant_rows(format, rounding)
+ * does (codes row-major with ldq bytes, scales[r]).  At least one of out and
+ * codes must be given.  The sum of squares is taken in a fixed order (lane l
+ * of a 64-lane group adds elements 8 (l + 64 i) + e in ascending (i, e), then
+ * a butterfly xor 32, 16, ..., 1 adds the lane sums) and rs is an IEEE square
+ * root followed by an IEEE division, so results are reproducible on a CPU;
+ * the reference's Triton rsqrt may differ in the last bits.
+ * bf16 tensors: value [rows, cols] (ldv), weight [cols], tables; indices
+ * int64 [rows] (not range-checked, as in the reference).  cols % 8 == 0,
+ * cols <= 8192, strides multiples of 8 elements, bf16 pointers 16-byte
+ * aligned, codes 8-byte aligned.
+ */
+int h3q_rms_norm_modulate_quant(const void* value, int64_t ldv, const void* weight, const void* scale,
+                                const void* shift, int64_t table_stride, const int64_t* indices, int64_t rows,
+                                int64_t cols, float eps, void* out, int64_t ldo, int format, int rounding, void* codes,
+                                int64_t ldq, float* scales, void* stream);
+
+/*
+ * The fc1-input producer fused_residual_gate_rms_norm_modulate
+ * (H3/inference/fused_kernels.py:319-357 kernel, 733-773 wrapper) with the
+ * same quantizer folded in: hidden = bf16(residual + bf16(gate[t, k] *
+ * branch)) is stored (ldh elements) and then normalized, modulated and
+ * quantized as in h3q_rms_norm_modulate_quant.
+ */
+int h3q_residual_gate_rms_norm_modulate_quant(const void* residual, int64_t ldr, const void* branch, int64_t ldb,
+                                              const void* gate, const void* weight, const void* scale,
+                                              const void* shift, int64_t table_stride, const int64_t* indices,
+                                              int64_t rows, int64_t cols, float eps, void* hidden, int64_t ldh,
+                                              void* out, int64_t ldo, int format, int rounding, void* codes,
+                                              int64_t ldq, float* scales, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,11 @@
  *                              model of the gfx950 FP8 matrix instruction, with a
  *                              bound on its remaining (combination) rounding
  *   orc_epilogue_*             s_a * (s_w * float(acc)) [+ bias] -> bf16 RNE
+ *   orc_rms_norm_modulate      H3/inference/fused_kernels.py:287-317 (RMSNorm + AdaLN
+ *                              modulate) and :319-357 (with the residual gate), with
+ *                              the sum-of-squares order and the IEEE rsqrt that the
+ *                              gfx950 kernel fixes (the reference's Triton rsqrt is
+ *                              approximate: parity with it is unpinned in the last bits)
  *
  * The e4m3fn and bf16 encoders are written from the format definitions (RNE on
  * an exact binary64 value); they are checked against torch's casts by the tests.
@@ -344,4 +349,76 @@ ORC_API void orc_epilogue_f64(const double* acc, int64_t ldacc, const float* s_a
             float v = bias ? fmaf(sa, t, orc_bf16_to_f32(bias[j])) : sa * t;
             out[i * ldo + j] = orc_f32_to_bf16(v);
         }
+}
+
+/* ------------------------------------------------- RMSNorm + AdaLN modulate */
+
+/* The reference's _round_bf16 (H3/inference/fused_kernels.py:65-68): add
+ * 0x7FFF plus the lowest kept bit to the binary32 bits and truncate. */
+static float round_bf16_ref(float f) {
+    uint32_t b = bits_from_f32(f);
+    return f32_from_bits((b + 0x7FFFu + ((b >> 16) & 1u)) & 0xFFFF0000u);
+}
+
+/* For each row r (t = indices[r]):
+ *   [branch] h = bf16(residual + bf16(gate[t] * branch))  -> hidden
+ *   v = branch ? h : value
+ *   ss: 64 lane sums, lane l adding v[8 (l + 64 i) + e]^2 (product rounded, then
+ *       the sum) in ascending (i, e); then 6 butterfly steps s_l += s_(l xor d),
+ *       d = 32, 16, ..., 1
+ *   rs = 1 / sqrt(ss / cols + eps)   (each operation an IEEE binary32 operation)
+ *   n  = bf16((v * rs) * weight);  y = bf16(bf16(n * bf16(1 + scale[t])) + shift[t])
+ * cols must be a multiple of 8.  hidden may be NULL without branch. */
+ORC_API void orc_rms_norm_modulate(const uint16_t* value, int64_t ldv, const uint16_t* branch, int64_t ldb,
+                                   const uint16_t* gate, const uint16_t* weight, const uint16_t* scale,
+                                   const uint16_t* shift, int64_t table_stride, const int64_t* indices,
+                                   int64_t rows, int64_t cols, float eps, uint16_t* hidden, int64_t ldh,
+                                   uint16_t* out, int64_t ldo) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        const int64_t t = indices[r];
+        float v[8192];
+        for (int64_t k = 0; k < cols; ++k) {
+            const float x = orc_bf16_to_f32(value[r * ldv + k]);
+            if (branch) {
+                const float g = orc_bf16_to_f32(gate[t * table_stride + k]);
+                const float b = orc_bf16_to_f32(branch[r * ldb + k]);
+                const float h = round_bf16_ref(x + round_bf16_ref(g * b));
+                v[k] = h;
+                if (hidden) hidden[r * ldh + k] = (uint16_t)(bits_from_f32(h) >> 16);
+            } else {
+                v[k] = x;
+            }
+        }
+        float lane[64];
+        const int64_t nvec = cols / 8;
+        for (int l = 0; l < 64; ++l) {
+            float s = 0.0f;
+            for (int64_t vec = l; vec < nvec; vec += 64)
+                for (int e = 0; e < 8; ++e) {
+                    const float x = v[8 * vec + e];
+                    const float sq = x * x;
+                    s = s + sq;
+                }
+            lane[l] = s;
+        }
+        for (int d = 32; d >= 1; d >>= 1) {
+            float nxt[64];
+            for (int l = 0; l < 64; ++l) nxt[l] = lane[l] + lane[l ^ d];
+            memcpy(lane, nxt, sizeof(lane));
+        }
+        const float mean = lane[0] / (float)cols;
+        const float root = sqrtf(mean + eps);
+        const float rs = 1.0f / root;
+        for (int64_t k = 0; k < cols; ++k) {
+            const float w = orc_bf16_to_f32(weight[k]);
+            const float sc = orc_bf16_to_f32(scale[t * table_stride + k]);
+            const float sh = orc_bf16_to_f32(shift[t * table_stride + k]);
+            const float vr = v[k] * rs;
+            const float n = round_bf16_ref(vr * w);
+            const float one_sc = round_bf16_ref(1.0f + sc);
+            const float y = round_bf16_ref(round_bf16_ref(n * one_sc) + sh);
+            out[r * ldo + k] = (uint16_t)(bits_from_f32(y) >> 16);
+        }
+    }
 }

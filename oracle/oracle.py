@@ -70,6 +70,9 @@ def _load() -> ctypes.CDLL:
     lib.orc_gemm_e4m3_f64.argtypes = [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64]
     lib.orc_gemm_e4m3_mfma.restype = None
     lib.orc_gemm_e4m3_mfma.argtypes = [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64]
+    lib.orc_rms_norm_modulate.argtypes = [_p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _p, _i64, _i64, ctypes.c_float,
+                                          _p, _i64, _p, _i64]
+    lib.orc_rms_norm_modulate.restype = None
     for name in ("orc_epilogue_i32", "orc_epilogue_f64"):
         fn = getattr(lib, name)
         fn.restype = None
@@ -284,6 +287,34 @@ def lora_down_reference(x_bits: np.ndarray, a_bits: np.ndarray) -> np.ndarray:
     x = bf16_to_f32(x_bits).astype(np.float64)
     a = bf16_to_f32(a_bits).astype(np.float64)
     return x @ a.T
+
+
+def rms_norm_modulate(value: np.ndarray, weight: np.ndarray, scale: np.ndarray, shift: np.ndarray,
+                      indices: np.ndarray, eps: float, residual_gate: tuple | None = None
+                      ) -> tuple[np.ndarray, np.ndarray | None]:
+    """bf16 bits in, (y bits [rows, cols], hidden bits or None): RMSNorm +
+    AdaLN modulate (+ residual gate) in the fixed order of the gfx950 kernel.
+    ``residual_gate = (branch_bits, gate_table_bits)`` makes ``value`` the residual."""
+    value = np.ascontiguousarray(value, dtype=np.uint16)
+    rows, cols = value.shape
+    if cols % 8 or cols > 8192:
+        raise ValueError("rms_norm_modulate: cols must be a multiple of 8, at most 8192")
+    weight = np.ascontiguousarray(weight, dtype=np.uint16).reshape(-1)
+    scale = np.ascontiguousarray(scale, dtype=np.uint16)
+    shift = np.ascontiguousarray(shift, dtype=np.uint16)
+    if scale.shape != shift.shape or scale.shape[1] != cols:
+        raise ValueError("rms_norm_modulate: tables must be [T, cols]")
+    indices = np.ascontiguousarray(indices, dtype=np.int64).reshape(-1)
+    out = np.empty((rows, cols), dtype=np.uint16)
+    branch = gate = hidden = None
+    if residual_gate is not None:
+        branch = np.ascontiguousarray(residual_gate[0], dtype=np.uint16)
+        gate = np.ascontiguousarray(residual_gate[1], dtype=np.uint16)
+        hidden = np.empty((rows, cols), dtype=np.uint16)
+    _load().orc_rms_norm_modulate(_ptr(value), cols, _ptr(branch), cols, _ptr(gate), _ptr(weight), _ptr(scale),
+                                 _ptr(shift), cols, _ptr(indices), rows, cols, ctypes.c_float(eps), _ptr(hidden),
+                                 cols, _ptr(out), cols)
+    return out, hidden
 
 
 def cpu_threads() -> int:

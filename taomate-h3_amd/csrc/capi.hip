@@ -58,6 +58,106 @@ __attribute__((visibility("default"))) int h3q_quant_rows(const void* x, int64_t
                         "h3q_quant_rows");
 }
 
+// Shared checks of the fused norm / modulate / quantize entry points.
+static int check_norm_quant(const char* who, int64_t rows, int64_t cols, int64_t table_stride, const void* weight,
+                            const void* scale, const void* shift, const int64_t* indices, const void* out,
+                            int64_t ldo, int format, int rounding, const void* codes, int64_t ldq,
+                            const float* scales) {
+    if (rows < 0 || cols <= 0) return fail(H3Q_ERR_INVALID, "%s: bad shape [%lld, %lld]", who, (long long)rows, (long long)cols);
+    if (cols % 8) return fail(H3Q_ERR_UNSUPPORTED, "%s: cols=%lld must be a multiple of 8", who, (long long)cols);
+    if (cols > h3q::kNormQuantMaxCols)
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: cols=%lld above %d", who, (long long)cols, h3q::kNormQuantMaxCols);
+    if (table_stride < cols || table_stride % 8)
+        return fail(H3Q_ERR_INVALID, "%s: table stride %lld must be >= cols and a multiple of 8", who,
+                    (long long)table_stride);
+    if (!out && !codes) return fail(H3Q_ERR_INVALID, "%s: neither a bf16 output nor codes requested", who);
+    if (out && (ldo < cols || ldo % 8)) return fail(H3Q_ERR_INVALID, "%s: bad output stride %lld", who, (long long)ldo);
+    if (codes) {
+        if (format != H3Q_FMT_E4M3FN && format != H3Q_FMT_INT8)
+            return fail(H3Q_ERR_INVALID, "%s: unknown format %d", who, format);
+        if (rounding != H3Q_ROUND_DIV && rounding != H3Q_ROUND_RCP_MUL)
+            return fail(H3Q_ERR_INVALID, "%s: unknown rounding %d", who, rounding);
+        if (format == H3Q_FMT_E4M3FN && rounding != H3Q_ROUND_DIV)
+            return fail(H3Q_ERR_UNSUPPORTED, "%s: e4m3fn codes use the division form only", who);
+        if (ldq < cols || ldq % 8) return fail(H3Q_ERR_INVALID, "%s: bad codes stride %lld", who, (long long)ldq);
+        if (!scales) return fail(H3Q_ERR_INVALID, "%s: codes need a scales pointer", who);
+        if (!aligned(codes, 8)) return fail(H3Q_ERR_INVALID, "%s: codes must be 8-byte aligned", who);
+    }
+    if (rows > 0 && (!weight || !scale || !shift || !indices)) return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
+    if (!aligned(weight, 16) || !aligned(scale, 16) || !aligned(shift, 16) || (out && !aligned(out, 16)))
+        return fail(H3Q_ERR_INVALID, "%s: bf16 operands must be 16-byte aligned", who);
+    return H3Q_OK;
+}
+
+__attribute__((visibility("default"))) int h3q_rms_norm_modulate_quant(
+    const void* value, int64_t ldv, const void* weight, const void* scale, const void* shift, int64_t table_stride,
+    const int64_t* indices, int64_t rows, int64_t cols, float eps, void* out, int64_t ldo, int format, int rounding,
+    void* codes, int64_t ldq, float* scales, void* stream) {
+    const char* who = "h3q_rms_norm_modulate_quant";
+    int rc = check_norm_quant(who, rows, cols, table_stride, weight, scale, shift, indices, out, ldo, format, rounding,
+                              codes, ldq, scales);
+    if (rc != H3Q_OK) return rc;
+    if (ldv < cols || ldv % 8) return fail(H3Q_ERR_INVALID, "%s: bad value stride %lld", who, (long long)ldv);
+    if (rows == 0) return ok();
+    if (!value || !aligned(value, 16)) return fail(H3Q_ERR_INVALID, "%s: value must be non-null and 16-byte aligned", who);
+    h3q::NormQuantArgs a{};
+    a.value = (const uint16_t*)value;
+    a.ldv = ldv;
+    a.weight = (const uint16_t*)weight;
+    a.scale = (const uint16_t*)scale;
+    a.shift = (const uint16_t*)shift;
+    a.table_stride = table_stride;
+    a.indices = indices;
+    a.rows = rows;
+    a.cols = (int)cols;
+    a.eps = eps;
+    a.out = (uint16_t*)out;
+    a.ldo = ldo;
+    a.codes = (uint8_t*)codes;
+    a.ldq = ldq;
+    a.scales = scales;
+    return check_launch(h3q::launch_norm_modulate_quant(a, false, format, rounding, (hipStream_t)stream), who);
+}
+
+__attribute__((visibility("default"))) int h3q_residual_gate_rms_norm_modulate_quant(
+    const void* residual, int64_t ldr, const void* branch, int64_t ldb, const void* gate, const void* weight,
+    const void* scale, const void* shift, int64_t table_stride, const int64_t* indices, int64_t rows, int64_t cols,
+    float eps, void* hidden, int64_t ldh, void* out, int64_t ldo, int format, int rounding, void* codes, int64_t ldq,
+    float* scales, void* stream) {
+    const char* who = "h3q_residual_gate_rms_norm_modulate_quant";
+    int rc = check_norm_quant(who, rows, cols, table_stride, weight, scale, shift, indices, out, ldo, format, rounding,
+                              codes, ldq, scales);
+    if (rc != H3Q_OK) return rc;
+    if (ldr < cols || ldr % 8 || ldb < cols || ldb % 8 || ldh < cols || ldh % 8)
+        return fail(H3Q_ERR_INVALID, "%s: bad residual / branch / hidden stride", who);
+    if (rows == 0) return ok();
+    if (!residual || !branch || !gate || !hidden) return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
+    if (!aligned(residual, 16) || !aligned(branch, 16) || !aligned(gate, 16) || !aligned(hidden, 16))
+        return fail(H3Q_ERR_INVALID, "%s: bf16 operands must be 16-byte aligned", who);
+    h3q::NormQuantArgs a{};
+    a.value = (const uint16_t*)residual;
+    a.ldv = ldr;
+    a.branch = (const uint16_t*)branch;
+    a.ldb = ldb;
+    a.gate = (const uint16_t*)gate;
+    a.weight = (const uint16_t*)weight;
+    a.scale = (const uint16_t*)scale;
+    a.shift = (const uint16_t*)shift;
+    a.table_stride = table_stride;
+    a.indices = indices;
+    a.rows = rows;
+    a.cols = (int)cols;
+    a.eps = eps;
+    a.hidden = (uint16_t*)hidden;
+    a.ldh = ldh;
+    a.out = (uint16_t*)out;
+    a.ldo = ldo;
+    a.codes = (uint8_t*)codes;
+    a.ldq = ldq;
+    a.scales = scales;
+    return check_launch(h3q::launch_norm_modulate_quant(a, true, format, rounding, (hipStream_t)stream), who);
+}
+
 __attribute__((visibility("default"))) int64_t h3q_tiled_bytes(int64_t rows, int64_t cols) {
     if (rows <= 0 || cols <= 0 || cols % 128) return 0;
     return (rows + 15) / 16 * (cols / 128) * 2048;

@@ -56,4 +56,29 @@ constexpr int64_t kSkinnyMaxM = 128;
 bool skinny_supported(const GemmArgs& a);
 hipError_t launch_gemm_skinny(int kind, const GemmArgs& a, hipStream_t st);
 
+// Fused RMSNorm + AdaLN modulate (+ residual gate) + per-token quantization
+// (norm_quant.hip).  All bf16 tensors are row-major with element strides;
+// tables are [T, table_stride] and row r uses table row indices[r].
+struct NormQuantArgs {
+    const uint16_t* value;   // [rows, cols]; with the residual gate: the residual
+    const uint16_t* branch;  // residual gate only: [rows, cols]
+    const uint16_t* gate;    // residual gate only: gate table
+    const uint16_t* weight;  // [cols] RMSNorm weight
+    const uint16_t* scale;   // modulate scale table
+    const uint16_t* shift;   // modulate shift table
+    const int64_t* indices;  // [rows]
+    int64_t ldv, ldb, table_stride, rows;
+    int cols;                // multiple of 8, at most 8192
+    float eps;
+    uint16_t* hidden;        // residual gate only: [rows, cols] out
+    int64_t ldh;
+    uint16_t* out;           // [rows, cols] bf16 modulated output, or null
+    int64_t ldo;
+    uint8_t* codes;          // [rows, cols] codes (row-major, ldq bytes), or null
+    int64_t ldq;
+    float* scales;           // [rows] per-token scales (with codes)
+};
+constexpr int kNormQuantMaxCols = 8192;
+hipError_t launch_norm_modulate_quant(const NormQuantArgs& a, bool resid, int fmt, int rounding, hipStream_t st);
+
 }  // namespace h3q

@@ -56,8 +56,17 @@ def current_parallel_context() -> ParallelContext:
 
 def _fp8_w8a8_linear(inputs: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
                      bias: torch.Tensor | None) -> torch.Tensor:
-    """Per-token dynamic e4m3fn activations x per-channel e4m3fn weights."""
+    """Per-token dynamic e4m3fn activations x per-channel e4m3fn weights
+    (the activations may come pre-quantized from a fused producer)."""
+    from ..inference.fused_kernels import QuantizedActivations
+
     shape = (*inputs.shape[:-1], int(weight.shape[0]))
+    if isinstance(inputs, QuantizedActivations):
+        if inputs.fmt != ops.FMT_E4M3FN:
+            raise TypeError("FP8 W8A8 linear expects e4m3fn activation codes")
+        out = ops.scaled_mm(inputs.codes, weight, inputs.scales.reshape(-1), weight_scale.reshape(-1), bias=bias,
+                            b_tiled=ops.is_tiled(weight), m=int(inputs.codes.shape[0]))
+        return out.reshape(shape)
     flat = inputs.reshape(-1, int(inputs.shape[-1])).contiguous()
     q, s, a_tiled = ops.quant_activations_for(flat, ops.FMT_E4M3FN, ops.ROUND_DIV, weight)
     out = ops.scaled_mm(q, weight, s.reshape(-1), weight_scale.reshape(-1), bias=bias, a_tiled=a_tiled,
@@ -85,8 +94,15 @@ def _fp8_tensor_linear(inputs: torch.Tensor, weight: torch.Tensor, weight_scale:
 
 
 def _module_linear(module: nn.Module, inputs: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
-    """H3/distributed/linear.py:15-33 plus the FP8 formats."""
+    """H3/distributed/linear.py:15-33 plus the FP8 formats.  ``inputs`` may
+    also be per-token codes from a fused producer (QuantizedActivations): the
+    per-token W8A8 paths consume them directly, the others use their bf16 rows."""
+    from ..inference.fused_kernels import QuantizedActivations, as_dense
+
     scale = getattr(module, "_cutlass_w8a8_weight_scale", None)
+    if isinstance(inputs, QuantizedActivations) and scale is None and \
+            getattr(module, "_fp8_w8a8_weight_scale", None) is None:
+        inputs = as_dense(inputs)
     if scale is not None:
         from ..inference.w8a8 import cutlass_w8a8_linear
 

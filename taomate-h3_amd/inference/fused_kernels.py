@@ -1,4 +1,5 @@
-"""FP8 quantizers of FL/inference/fused_kernels.py:771-820 on gfx950.
+"""FP8 quantizers of FL/inference/fused_kernels.py:771-820 and the
+RMSNorm/AdaLN producers of H3/inference/fused_kernels.py:700-773 on gfx950.
 
 Same names, arguments and results as the reference; the Triton kernels
 (amax partial/finalize + quantize, three launches) are replaced by
@@ -12,9 +13,21 @@ quotient rounded to bf16 before the e4m3fn cast.
 per-token x per-channel FP8 W8A8 linear: fp32 quotient, scale
 ``max(amax_row / 448, 1e-12)``.  There is no bf16 fallback: inputs must be
 bf16 tensors on a ROCm device.
+
+``fused_rms_norm_modulate`` and ``fused_residual_gate_rms_norm_modulate``
+keep the reference's names, arguments, results and index check.  Their
+``*_w8a8`` variants run the same kernel with the per-token activation
+quantizer of the next W8A8 linear folded in and return a
+``QuantizedActivations`` that ``cutlass_w8a8_linear`` accepts in place of the
+bf16 input, so the QKV / fc1 input is never written and re-read in bf16.  The
+sum of squares and rsqrt are computed in a fixed order with IEEE operations
+(the reference's Triton kernels use an approximate rsqrt); see
+include/taomate_h3_amd.h.
 """
 
 from __future__ import annotations
+
+from dataclasses import dataclass
 
 import torch
 
@@ -56,4 +69,101 @@ def quantize_fp8_e4m3_rowwise(value: torch.Tensor) -> tuple[torch.Tensor, torch.
     return codes.reshape(shape), scales.reshape(*shape[:-1], 1)
 
 
-__all__ = ["FP8_MAX", "quantize_fp8_e4m3", "quantize_fp8_e4m3_dynamic", "quantize_fp8_e4m3_rowwise"]
+@dataclass
+class QuantizedActivations:
+    """Per-token codes of a linear's input: ``codes [M, K]`` (row-major),
+    ``scales [M, 1]`` fp32, the activation ``shape [..., K]`` they stand for,
+    the code format, and optionally the bf16 rows themselves (``dense``, for a
+    LoRA side branch that needs them)."""
+
+    codes: torch.Tensor
+    scales: torch.Tensor
+    shape: tuple
+    fmt: int = ops.FMT_INT8
+    dense: torch.Tensor | None = None
+
+
+def as_dense(inputs):
+    """The bf16 activations behind ``inputs`` (a tensor, or a
+    QuantizedActivations produced with ``keep_dense=True``)."""
+    if not isinstance(inputs, QuantizedActivations):
+        return inputs
+    if inputs.dense is None:
+        raise TypeError("this linear needs the bf16 activations; produce them with keep_dense=True")
+    return inputs.dense.reshape(inputs.shape)
+
+
+def _modulation_inputs(value: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, indices: torch.Tensor,
+                       what: str):
+    flat = value.reshape(-1, int(value.shape[-1]))
+    if flat.stride(-1) != 1 or (flat.shape[0] > 1 and flat.stride(0) % 8):
+        flat = flat.contiguous()
+    index = indices.reshape(-1)
+    if int(index.numel()) != int(flat.shape[0]):
+        raise ValueError(f"SOL {what} indices do not cover every row")
+    index = index.to(torch.int64).contiguous()
+    if scale.stride(-1) != 1 or shift.stride(-1) != 1:
+        scale, shift = scale.contiguous(), shift.contiguous()
+    return flat, index, scale, shift
+
+
+def fused_rms_norm_modulate(value: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                            indices: torch.Tensor, eps: float) -> torch.Tensor:
+    """bf16(bf16(RMSNorm(value) * bf16(1 + scale[idx])) + shift[idx])
+    (H3/inference/fused_kernels.py:700-730)."""
+    _as_bf16(value, "fused_rms_norm_modulate")
+    flat, index, scale, shift = _modulation_inputs(value, scale, shift, indices, "RMSNorm/AdaLN")
+    out, _, _ = ops.norm_modulate_quant(flat, weight.contiguous(), scale, shift, index, eps, out=True)
+    return out.reshape(value.shape)
+
+
+def fused_residual_gate_rms_norm_modulate(residual: torch.Tensor, branch: torch.Tensor, gate: torch.Tensor,
+                                          weight: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                                          indices: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(hidden, output): hidden = bf16(residual + bf16(gate[idx] * branch)),
+    output = the modulated RMSNorm of hidden (H3/inference/fused_kernels.py:733-773)."""
+    _as_bf16(residual, "fused_residual_gate_rms_norm_modulate")
+    flat, index, scale, shift = _modulation_inputs(residual, scale, shift, indices, "residual/AdaLN")
+    branch_flat = branch.reshape(-1, int(branch.shape[-1])).contiguous()
+    gate = gate.contiguous() if gate.stride(-1) != 1 else gate
+    hidden = torch.empty_like(flat)
+    out, _, _ = ops.norm_modulate_quant(flat, weight.contiguous(), scale, shift, index, eps, out=True,
+                                        residual_gate=(branch_flat, gate, hidden))
+    return hidden.reshape(residual.shape), out.reshape(residual.shape)
+
+
+def fused_rms_norm_modulate_w8a8(value: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
+                                 shift: torch.Tensor, indices: torch.Tensor, eps: float, *,
+                                 fmt: int = ops.FMT_INT8, keep_dense: bool = False) -> QuantizedActivations:
+    """``fused_rms_norm_modulate`` whose output goes straight into per-token
+    codes for the next W8A8 linear (int8 in the vLLM form, or e4m3fn)."""
+    _as_bf16(value, "fused_rms_norm_modulate_w8a8")
+    flat, index, scale, shift = _modulation_inputs(value, scale, shift, indices, "RMSNorm/AdaLN")
+    rounding = ops.ROUND_RCP_MUL if fmt == ops.FMT_INT8 else ops.ROUND_DIV
+    dense, codes, scales = ops.norm_modulate_quant(flat, weight.contiguous(), scale, shift, index, eps,
+                                                   fmt=fmt, rounding=rounding, out=bool(keep_dense))
+    return QuantizedActivations(codes, scales, tuple(value.shape), fmt, dense)
+
+
+def fused_residual_gate_rms_norm_modulate_w8a8(residual: torch.Tensor, branch: torch.Tensor, gate: torch.Tensor,
+                                               weight: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                                               indices: torch.Tensor, eps: float, *, fmt: int = ops.FMT_INT8,
+                                               keep_dense: bool = False
+                                               ) -> tuple[torch.Tensor, QuantizedActivations]:
+    """``fused_residual_gate_rms_norm_modulate`` with the modulated output
+    quantized per token: (hidden, QuantizedActivations)."""
+    _as_bf16(residual, "fused_residual_gate_rms_norm_modulate_w8a8")
+    flat, index, scale, shift = _modulation_inputs(residual, scale, shift, indices, "residual/AdaLN")
+    branch_flat = branch.reshape(-1, int(branch.shape[-1])).contiguous()
+    gate = gate.contiguous() if gate.stride(-1) != 1 else gate
+    hidden = torch.empty_like(flat)
+    rounding = ops.ROUND_RCP_MUL if fmt == ops.FMT_INT8 else ops.ROUND_DIV
+    dense, codes, scales = ops.norm_modulate_quant(flat, weight.contiguous(), scale, shift, index, eps, fmt=fmt,
+                                                   rounding=rounding, out=bool(keep_dense),
+                                                   residual_gate=(branch_flat, gate, hidden))
+    return hidden.reshape(residual.shape), QuantizedActivations(codes, scales, tuple(residual.shape), fmt, dense)
+
+
+__all__ = ["FP8_MAX", "QuantizedActivations", "as_dense", "fused_residual_gate_rms_norm_modulate",
+           "fused_residual_gate_rms_norm_modulate_w8a8", "fused_rms_norm_modulate", "fused_rms_norm_modulate_w8a8",
+           "quantize_fp8_e4m3", "quantize_fp8_e4m3_dynamic", "quantize_fp8_e4m3_rowwise"]

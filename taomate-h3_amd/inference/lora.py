@@ -87,6 +87,9 @@ class H3InferenceParallelLinearLoRA(torch.nn.Module):
         self.register_buffer("lora_b", b, persistent=False)
 
     def forward(self, inputs: torch.Tensor) -> torch.Tensor:
+        from .fused_kernels import as_dense
+
+        inputs = as_dense(inputs)  # the LoRA branch needs the bf16 rows
         if _fusable(self.base, self.lora_a, self.lora_b):
             return fused_quantized_lora_linear(self.base, inputs, self.lora_a, self.lora_b, self.scale)
         output = self.base(inputs)

@@ -214,6 +214,10 @@ def cutlass_w8a8_linear(inputs: torch.Tensor, weight: torch.Tensor, weight_scale
     (H3/inference/w8a8.py:190-220)."""
     if bias is not None:
         raise RuntimeError("H3 W8A8 supports bias-free linears only")
+    from .fused_kernels import QuantizedActivations
+
+    if isinstance(inputs, QuantizedActivations):
+        return _linear_from_codes(inputs, weight, weight_scale, workspace)
     shape = (*inputs.shape[:-1], int(weight.shape[0]))
     flattened = inputs.reshape(-1, int(inputs.shape[-1])).contiguous()
     if workspace is not None:
@@ -232,6 +236,22 @@ def cutlass_w8a8_linear(inputs: torch.Tensor, weight: torch.Tensor, weight_scale
     backend = require_vllm_cutlass_w8a8()
     quantized, activation_scale, _ = backend.scaled_int8_quant(flattened)
     output = backend.cutlass_scaled_mm(quantized, weight.t(), activation_scale, weight_scale.t(), torch.bfloat16)
+    return output.reshape(shape)
+
+
+def _linear_from_codes(inputs: Any, weight: torch.Tensor, weight_scale: torch.Tensor,
+                       workspace: CutlassW8A8Workspace | None) -> torch.Tensor:
+    """The W8A8 GEMM on activations already quantized per token (int8, vLLM
+    form) by a fused producer: the act-quant pass of the linear is skipped."""
+    if inputs.fmt != ops.FMT_INT8 or inputs.codes.dtype != torch.int8:
+        raise TypeError("H3 W8A8 linear expects int8 activation codes")
+    rows = int(inputs.codes.shape[0])
+    shape = (*inputs.shape[:-1], int(weight.shape[0]))
+    out = None
+    if workspace is not None:
+        _, _, out = workspace.buffers(inputs.codes, int(weight.shape[0]))
+    output = ops.scaled_mm(inputs.codes, weight, inputs.scales.reshape(-1), weight_scale.reshape(-1), out=out,
+                           b_tiled=ops.is_tiled(weight), m=rows)
     return output.reshape(shape)
 
 

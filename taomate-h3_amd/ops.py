@@ -81,6 +81,87 @@ def quant_rows(x: torch.Tensor, fmt: int, rounding: int = ROUND_DIV, *, codes: t
     return codes, scales
 
 
+def _table(name: str, t: torch.Tensor, cols: int) -> int:
+    """A [T, stride] bf16 modulation table (rows 16-byte aligned); returns its row stride."""
+    _rows_2d(name, t, torch.bfloat16)
+    if t.shape[1] != cols:
+        raise ValueError(f"{name}: expected {cols} columns, got {t.shape[1]}")
+    stride = t.stride(0) if t.shape[0] > 1 else cols
+    if stride % 8:
+        raise ValueError(f"{name}: row stride {stride} must be a multiple of 8 elements")
+    return stride
+
+
+def norm_modulate_quant(value: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                        indices: torch.Tensor, eps: float, *, fmt: int | None = None, rounding: int = ROUND_DIV,
+                        out: torch.Tensor | bool | None = None, codes: torch.Tensor | None = None,
+                        scales: torch.Tensor | None = None, residual_gate: tuple | None = None):
+    """RMSNorm + AdaLN modulate of bf16 rows, optionally preceded by the
+    residual gate and followed by per-token quantization, in one kernel.
+
+    ``value [rows, cols]`` (the residual when ``residual_gate=(branch, gate,
+    hidden)`` is given: hidden = bf16(residual + bf16(gate[t] * branch)) is
+    written into ``hidden``), ``weight [cols]``, ``scale``/``shift`` (and
+    ``gate``) tables ``[T, cols]`` selected per row by int64 ``indices
+    [rows]``.  ``out``: a bf16 tensor to receive the modulated rows, True to
+    allocate one, None/False for none.  ``fmt``: code format for the per-token
+    quantization (None: no codes).  Returns (out or None, codes or None,
+    scales or None)."""
+    branch = gate = hidden = None
+    if residual_gate is not None:
+        branch, gate, hidden = residual_gate
+    want_out = out is True or isinstance(out, torch.Tensor)
+    _require_gpu("norm_modulate_quant", value, weight, scale, shift, indices, branch, gate, hidden,
+                 out if isinstance(out, torch.Tensor) else None, codes, scales)
+    _rows_2d("norm_modulate_quant value", value, torch.bfloat16)
+    rows, cols = value.shape
+    if weight.dtype != torch.bfloat16 or weight.numel() != cols or not weight.is_contiguous():
+        raise ValueError("norm_modulate_quant: weight must be a contiguous bf16 vector of the row width")
+    stride = _table("norm_modulate_quant scale", scale, cols)
+    if _table("norm_modulate_quant shift", shift, cols) != stride:
+        raise ValueError("norm_modulate_quant: scale and shift tables differ in row stride")
+    if indices.dtype != torch.int64 or indices.numel() != rows or not indices.is_contiguous():
+        raise ValueError("norm_modulate_quant: indices must be a contiguous int64 tensor with one entry per row")
+    if out is True:
+        out = torch.empty((rows, cols), device=value.device, dtype=torch.bfloat16)
+    elif not want_out:
+        out = None
+    if out is not None:
+        _rows_2d("norm_modulate_quant out", out, torch.bfloat16)
+        if tuple(out.shape) != (rows, cols):
+            raise ValueError("norm_modulate_quant: out shape mismatch")
+    if fmt is not None:
+        if codes is None:
+            codes = torch.empty((rows, cols), device=value.device, dtype=_CODE_DTYPES[fmt])
+        if scales is None:
+            scales = torch.empty((rows, 1), device=value.device, dtype=torch.float32)
+        _rows_2d("norm_modulate_quant codes", codes, _CODE_DTYPES[fmt])
+        if tuple(codes.shape) != (rows, cols):
+            raise ValueError("norm_modulate_quant: codes shape mismatch")
+        if scales.dtype != torch.float32 or scales.numel() != rows or not scales.is_contiguous():
+            raise ValueError("norm_modulate_quant: scales must be a contiguous fp32 tensor with one entry per row")
+    elif codes is not None or scales is not None:
+        raise ValueError("norm_modulate_quant: codes / scales given without a format")
+    if out is None and fmt is None:
+        raise ValueError("norm_modulate_quant: neither a bf16 output nor codes requested")
+    ld = lambda t: (t.stride(0) if rows > 1 else cols) if t is not None else cols
+    common = (_ptr(weight), _ptr(scale), _ptr(shift), stride, _ptr(indices), rows, cols, float(eps))
+    tail = (_ptr(out), ld(out), FMT_INT8 if fmt is None else fmt, rounding, _ptr(codes), ld(codes), _ptr(scales),
+            _stream(value))
+    if residual_gate is None:
+        _lib.call("h3q_rms_norm_modulate_quant", _ptr(value), ld(value), *common, *tail)
+    else:
+        _rows_2d("norm_modulate_quant branch", branch, torch.bfloat16)
+        _rows_2d("norm_modulate_quant hidden", hidden, torch.bfloat16)
+        if tuple(branch.shape) != (rows, cols) or tuple(hidden.shape) != (rows, cols):
+            raise ValueError("norm_modulate_quant: branch / hidden shape mismatch")
+        if _table("norm_modulate_quant gate", gate, cols) != stride:
+            raise ValueError("norm_modulate_quant: gate table row stride differs from scale / shift")
+        _lib.call("h3q_residual_gate_rms_norm_modulate_quant", _ptr(value), ld(value), _ptr(branch), ld(branch),
+                  _ptr(gate), *common, _ptr(hidden), ld(hidden), *tail)
+    return out, codes, scales
+
+
 def can_tile(rows: int, cols: int) -> bool:
     """Whether a [rows, cols] weight is stored tiled by the module mirror:
     the tiled matrix then has exactly the row-major shape and byte count."""

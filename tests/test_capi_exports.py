@@ -22,7 +22,8 @@ def _declared() -> set[str]:
 def test_header_declares_entry_points():
     names = _declared()
     assert {"h3q_quant_rows", "h3q_quant_tensor_e4m3", "h3q_scaled_mm", "h3q_gemm_i8_i32",
-            "h3q_lora_down", "h3q_last_error", "h3q_version", "h3q_tiled_bytes", "h3q_quant_rows_tiled"} <= names
+            "h3q_lora_down", "h3q_last_error", "h3q_version", "h3q_tiled_bytes", "h3q_quant_rows_tiled",
+            "h3q_rms_norm_modulate_quant", "h3q_residual_gate_rms_norm_modulate_quant"} <= names
 
 
 def test_library_exports_every_declared_symbol():
@@ -66,3 +67,31 @@ def test_version_and_error_without_gpu():
     rc = lib.h3q_quant_rows_tiled(None, 4, 100, 100, 0, 0, 0, None, None, None)
     assert rc == 1 and b"multiple of 128" in lib.h3q_last_error()
     assert lib.h3q_tiled_bytes(17, 256) == 2 * 2 * 2048 and lib.h3q_tiled_bytes(16, 100) == 0
+
+
+def test_norm_quant_errors_without_gpu():
+    """The fused norm / modulate / quantize entry points reject bad requests
+    on the host (no launch)."""
+    from taomate_h3_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("library not built")
+    lib = _lib.lib()
+    f = ctypes.c_float(1e-6)
+    # cols not a multiple of 8
+    rc = lib.h3q_rms_norm_modulate_quant(None, 12, None, None, None, 12, None, 4, 12, f, None, 12, 1, 1, None, 12,
+                                         None, None)
+    assert rc == 2 and b"multiple of 8" in lib.h3q_last_error()
+    # neither output nor codes
+    rc = lib.h3q_rms_norm_modulate_quant(None, 16, None, None, None, 16, None, 4, 16, f, None, 16, 1, 1, None, 16,
+                                         None, None)
+    assert rc == 1 and b"neither" in lib.h3q_last_error()
+    # e4m3 codes only in the division form
+    rc = lib.h3q_residual_gate_rms_norm_modulate_quant(None, 16, None, 16, None, None, None, None, 16, None, 4, 16,
+                                                       f, None, 16, None, 16, 0, 1, ctypes.c_void_p(64), 16,
+                                                       ctypes.c_void_p(64), None)
+    assert rc == 2 and b"division form" in lib.h3q_last_error()
+    # width limit
+    rc = lib.h3q_rms_norm_modulate_quant(None, 8200, None, None, None, 8200, None, 4, 8200, f, ctypes.c_void_p(64),
+                                         8200, 1, 1, None, 8200, None, None)
+    assert rc == 2 and b"above 8192" in lib.h3q_last_error()

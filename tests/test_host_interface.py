@@ -159,3 +159,25 @@ def test_int8_stream_chunking_matches_whole_matrix_on_host_formula():
 
     assert np.array_equal(np.concatenate([p[0] for p in parts]), whole_q)
     assert np.array_equal(np.concatenate([p[1] for p in parts]), whole_s)
+
+
+def test_fused_norm_mirrors_check_indices_and_devices():
+    """fused_rms_norm_modulate keeps the reference's index check
+    (H3/inference/fused_kernels.py:711-713) and, like every op here, refuses
+    host tensors before any launch."""
+    from taomate_h3_amd.inference import fused_kernels as fk
+
+    x = torch.zeros(2, 3, 16, dtype=torch.bfloat16)
+    w = torch.ones(16, dtype=torch.bfloat16)
+    tab = torch.zeros(2, 16, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="SOL RMSNorm/AdaLN indices do not cover every row"):
+        fk.fused_rms_norm_modulate(x, w, tab, tab, torch.zeros(5, dtype=torch.int64), 1e-6)
+    with pytest.raises(ValueError, match="SOL residual/AdaLN indices do not cover every row"):
+        fk.fused_residual_gate_rms_norm_modulate(x, x, tab, w, tab, tab, torch.zeros(7, dtype=torch.int64), 1e-6)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fk.fused_rms_norm_modulate(x, w, tab, tab, torch.zeros(6, dtype=torch.int64), 1e-6)
+    with pytest.raises(TypeError, match="bfloat16"):
+        fk.fused_rms_norm_modulate_w8a8(x.float(), w, tab, tab, torch.zeros(6, dtype=torch.int64), 1e-6)
+    qa = fk.QuantizedActivations(torch.zeros(6, 16, dtype=torch.int8), torch.ones(6, 1), (2, 3, 16))
+    with pytest.raises(TypeError, match="keep_dense=True"):
+        fk.as_dense(qa)

@@ -347,3 +347,105 @@ def test_to_tiled_places_single_codes():
         flat = to_tiled(a).ravel()
         off = ((r // 16) * 2 + k // 128) * 2048 + (k % 32 // 16) * 1024 + (r % 16 + 16 * (k % 128 // 32)) * 16 + k % 16
         assert np.nonzero(flat)[0].tolist() == [off], (r, k)
+
+
+# ---------------------------------------------- RMSNorm + AdaLN modulate oracle
+
+def _norm_inputs(rows, cols, t, seed):
+    gen = torch.Generator().manual_seed(seed)
+    x = activations(rows, cols, seed=seed, outlier_channels=max(1, cols // 100), outlier_scale=10.0)
+    branch = activations(rows, cols, seed=seed + 1)
+    weight = (1.0 + 0.1 * torch.randn(cols, generator=gen)).to(torch.bfloat16)
+    scale = (0.2 * torch.randn(t, cols, generator=gen)).to(torch.bfloat16)
+    shift = (0.2 * torch.randn(t, cols, generator=gen)).to(torch.bfloat16)
+    gate = (1.0 + 0.5 * torch.randn(t, cols, generator=gen)).to(torch.bfloat16)
+    idx = torch.randint(0, t, (rows,), generator=gen, dtype=torch.int64)
+    return x, branch, weight, scale, shift, gate, idx
+
+
+def _ulps_bf16(a_bits, b_bits):
+    """Distance in bf16 units in the last place (same-sign finite values)."""
+    a = a_bits.astype(np.int32)
+    b = b_bits.astype(np.int32)
+    a = np.where(a & 0x8000, 0x8000 - a, a)
+    b = np.where(b & 0x8000, 0x8000 - b, b)
+    return np.abs(a - b)
+
+
+@pytest.mark.parametrize("resid", [False, True])
+def test_norm_modulate_matches_reference_eager_expression(oracle, resid):
+    """The reference's non-fused path evaluated by torch on the CPU:
+    nn.RMSNorm (H3/model/layers.py:74-92), then value * (1 + scale[idx]) +
+    shift[idx] in bf16 (layers.py:100-117), with the residual gate
+    (residual + gate[idx] * branch).to(bf16) (layers.py:120-135) first.
+    hidden is bit-exact (bf16 elementwise ops).  The normalized rows (zero
+    tables) differ only where torch's rsqrt / mean round differently from the
+    fixed IEEE order: at most 1 bf16 ulp, on a small fraction of elements.
+    Given the oracle's normalized rows, torch's modulation reproduces the
+    oracle's modulated rows bit for bit."""
+    rows, cols, t = 64, 2048, 3
+    x, branch, weight, scale, shift, gate, idx = _norm_inputs(rows, cols, t, 5)
+    eps = 1e-6
+    rg = (bits16(branch), bits16(gate)) if resid else None
+    norm = torch.nn.RMSNorm(cols, eps=eps, dtype=torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_(weight)
+        h = (x + gate.index_select(0, idx) * branch).to(torch.bfloat16) if resid else x
+        normed = norm(h).to(torch.bfloat16)
+    zeros = np.zeros((t, cols), dtype=np.uint16)
+    n_bits, hid = oracle.rms_norm_modulate(bits16(x), bits16(weight), zeros, zeros, idx.numpy(), eps,
+                                           residual_gate=rg)
+    if resid:
+        np.testing.assert_array_equal(hid, bits16(h))
+    d = _ulps_bf16(n_bits, bits16(normed))
+    assert d.max() <= 1, d.max()
+    assert (d == 0).mean() > 0.98, (d == 0).mean()
+    y, _ = oracle.rms_norm_modulate(bits16(x), bits16(weight), bits16(scale), bits16(shift), idx.numpy(), eps,
+                                    residual_gate=rg)
+    n = from_bits16(n_bits)
+    ref = (n * (1.0 + scale.index_select(0, idx)) + shift.index_select(0, idx)).to(torch.bfloat16)
+    np.testing.assert_array_equal(y, bits16(ref))
+
+
+def test_norm_closed_forms(oracle):
+    """Constant rows normalize to exactly +-1 (eps = 0, unit weight, no
+    modulation); a zero row gives the shift row; scale = -1 gives the shift
+    row; scaling a row by a power of two leaves the output unchanged (eps = 0);
+    gate = 0 keeps the residual and residual = 0 with gate = 1 yields the
+    branch."""
+    cols = 256
+    one = np.full(cols, 0x3F80, dtype=np.uint16)           # bf16 1.0
+    zero_tab = np.zeros((2, cols), dtype=np.uint16)
+    vals = [0.75, -3.0, 2.0 ** -20, 1000.0]
+    x = oracle.f32_to_bf16(np.repeat(np.array(vals, dtype=np.float32)[:, None], cols, 1))
+    y, _ = oracle.rms_norm_modulate(x, one, zero_tab, zero_tab, np.zeros(len(vals), np.int64), 0.0)
+    np.testing.assert_array_equal(oracle.bf16_to_f32(y), np.sign(np.array(vals, np.float32))[:, None] * np.ones(cols))
+
+    rng = np.random.default_rng(3)
+    shift = oracle.f32_to_bf16(rng.standard_normal((2, cols)).astype(np.float32))
+    scale = oracle.f32_to_bf16(rng.standard_normal((2, cols)).astype(np.float32))
+    scale[1] = oracle.f32_to_bf16(np.float32(-1.0))
+    xr = oracle.f32_to_bf16(rng.standard_normal((3, cols)).astype(np.float32))
+    xr[0] = 0
+    weight = oracle.f32_to_bf16((1 + 0.1 * rng.standard_normal(cols)).astype(np.float32))
+    y, _ = oracle.rms_norm_modulate(xr, weight, scale, shift, np.array([0, 1, 1], np.int64), 1e-6)
+    np.testing.assert_array_equal(y[0], shift[0])
+    np.testing.assert_array_equal(y[1], shift[1])
+    np.testing.assert_array_equal(y[2], shift[1])
+
+    xs = oracle.f32_to_bf16(rng.standard_normal((4, cols)).astype(np.float32))
+    x4 = oracle.f32_to_bf16(oracle.bf16_to_f32(xs) * np.float32(4.0))
+    idx = np.array([0, 1, 0, 1], np.int64)
+    y1, _ = oracle.rms_norm_modulate(xs, weight, scale, shift, idx, 0.0)
+    y2, _ = oracle.rms_norm_modulate(x4, weight, scale, shift, idx, 0.0)
+    np.testing.assert_array_equal(y1, y2)
+
+    res = oracle.f32_to_bf16(rng.standard_normal((2, cols)).astype(np.float32))
+    br = oracle.f32_to_bf16(rng.standard_normal((2, cols)).astype(np.float32))
+    gates = np.stack([np.zeros(cols, np.uint16), one])
+    _, hid = oracle.rms_norm_modulate(res, weight, scale, shift, np.array([0, 0], np.int64), 1e-6,
+                                      residual_gate=(br, gates))
+    np.testing.assert_array_equal(hid, res)
+    _, hid = oracle.rms_norm_modulate(np.zeros_like(res), weight, scale, shift, np.array([1, 1], np.int64), 1e-6,
+                                      residual_gate=(br, gates))
+    np.testing.assert_array_equal(hid, br)
