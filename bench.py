@@ -209,6 +209,43 @@ def bench_f1(torch, ops, dev) -> dict:
     return res
 
 
+def bench_f4(torch, ops, dev) -> dict:
+    """Next row (f)4: per-(batch, head) FP8 quantization of one attention
+    operand, [1, 8192, 56, 128] bf16 (the FL transformer's 56 heads of 128 at
+    one GPU), four rotating inputs.  Algorithmic bytes: 2 in + 1 out per
+    element (the kernel reads the input twice: per-head maxima, then
+    quantization).  Beside it, the same expression in eager torch on the GPU
+    (what the reference runs without Triton: amax, divide, clamp, cast)."""
+    gen = torch.Generator(device=dev).manual_seed(0)
+    shape = (1, 8192, 56, 128)
+    xs = [gpu_randn(torch, shape, gen, dev) for _ in range(4)]
+    n = xs[0].numel()
+    codes = torch.empty(shape, device=dev, dtype=torch.float8_e4m3fn)
+    scales = torch.empty(shape[0], shape[2], device=dev, dtype=torch.float32)
+    ws = torch.empty(int(ops._lib.lib().h3q_quant_per_head_workspace_floats(*shape)), device=dev,
+                     dtype=torch.float32)
+
+    def native(i):
+        ops.quant_per_head_e4m3(xs[i % 4], codes=codes, scales=scales, workspace=ws)
+
+    def eager(i):
+        v = xs[i % 4]
+        sc = torch.clamp(v.float().abs().amax(dim=(1, 3)) / 448.0, min=1.0e-12)
+        torch.clamp(v / sc[:, None, :, None], -448.0, 448.0).to(torch.float8_e4m3fn)
+
+    for fn in (native, eager):
+        for i in range(4):
+            fn(i)
+    torch.cuda.synchronize()
+    t_native = time_events(torch, native, 40) * 1e3
+    t_eager = time_events(torch, eager, 5) * 1e3
+    byts = 3 * n + 4 * shape[0] * shape[2]
+    del xs, codes
+    return {"shape": list(shape), "us": round(t_native, 1), "GB/s": round(byts / t_native / 1e3, 1),
+            "frac_hbm": round(byts / t_native / 1e3 / HBM_PEAK_GBS, 3), "algorithmic_bytes": byts,
+            "torch_eager_us": round(t_eager, 1)}
+
+
 def bench_c5(torch, ops, dev) -> dict:
     """int8 W8A8 at 1080p, M=40960, K=N=5120: per-token
     int8 act quant (vLLM formula) + int32-exact GEMM with fused dequant."""
@@ -414,7 +451,7 @@ def main() -> int:
     del xs, w, q_w, q_a, out
     torch.cuda.empty_cache()
     if not args.no_extra:
-        log("secondary configs: c3, c4, c5, f1")
+        log("secondary configs: c3, c4, c5, f1, f4")
         result["c3"] = bench_c3(torch, ops, dev)
         torch.cuda.empty_cache()
         result["c4"] = bench_c4(torch, ops, dev)
@@ -422,6 +459,8 @@ def main() -> int:
         result["c5"] = bench_c5(torch, ops, dev)
         torch.cuda.empty_cache()
         result["f1"] = bench_f1(torch, ops, dev)
+        torch.cuda.empty_cache()
+        result["f4"] = bench_f4(torch, ops, dev)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(torch, w_cpu, bias_cpu, x_cpu)

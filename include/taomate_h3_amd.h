@@ -27,7 +27,7 @@ extern "C" {
 #define H3Q_FMT_INT8 1   /* symmetric int8 */
 
 /* Rounding forms of the per-row quantizer. */
-#define H3Q_ROUND_DIV 0     /* q = round(x / s), s = max(amax / L, 1e-12)  (reference weight quantizer) */
+#define H3Q_ROUND_DIV 0     /* q = round(x / s), s = max(amax * RN(1/L), 1e-12)  (reference weight quantizer) */
 #define H3Q_ROUND_RCP_MUL 1 /* q = sat8(rint(x * (127 / amax))), s = amax / 127  (vLLM dynamic int8) */
 
 /* Scale granularities of the scaled GEMM. */
@@ -55,9 +55,13 @@ const char* h3q_last_error(void);
  * dimension ldx elements) into codes [rows, cols] (leading dimension ldq
  * bytes) and fp32 scales [rows].
  *
- *   format=E4M3FN, rounding=DIV : s = max(amax/448, 1e-12), q = e4m3(clamp(x/s, +-448))
- *   format=INT8,   rounding=DIV : s = max(amax/127, 1e-12), q = clamp(rne(x/s), +-127)
+ *   format=E4M3FN, rounding=DIV : s = max(amax*RN(1/448), 1e-12), q = e4m3(clamp(x/s, +-448))
+ *   format=INT8,   rounding=DIV : s = max(amax*RN(1/127), 1e-12), q = clamp(rne(x/s), +-127)
  *   format=INT8,   rounding=RCP_MUL : s = amax/127, q = sat8(rne(x * (127/amax))), zero row -> 0
+ *
+ * DIV scales are the reference's torch.clamp(amax.float() / L, min=1e-12) as
+ * PyTorch evaluates it on the GPU (a tensor divided by a Python scalar is a
+ * multiply by the binary32 reciprocal of the scalar); x/s is IEEE division.
  *
  * Replaces vLLM torch.ops._C.dynamic_scaled_int8_quant(out, in, scales, None)
  * (called at H3/inference/w8a8.py:178 and, allocating, :212) with RCP_MUL,
@@ -96,7 +100,7 @@ int h3q_quant_rows_tiled(const void* x, int64_t rows, int64_t cols, int64_t ldx,
 
 /*
  * Per-tensor e4m3fn quantization with a bf16 intermediate:
- *   s = static_scale ? *static_scale : max(amax(|x|)/448, 1e-12)
+ *   s = static_scale ? *static_scale : max(amax(|x|) * RN(1/448), 1e-12)
  *   q = e4m3(clamp(bf16(x / s), +-448));  *scale_out = s
  * Replaces quantize_fp8_e4m3_dynamic / quantize_fp8_e4m3
  * (FL/inference/fused_kernels.py:771-820) and the per-tensor FP8 weight
@@ -107,6 +111,41 @@ int h3q_quant_rows_tiled(const void* x, int64_t rows, int64_t cols, int64_t ldx,
 int64_t h3q_quant_tensor_workspace_floats(int64_t rows, int64_t cols);
 int h3q_quant_tensor_e4m3(const void* x, int64_t rows, int64_t cols, int64_t ldx, const float* static_scale,
                           float* partial, void* codes, int64_t ldq, float* scale_out, void* stream);
+
+/*
+ * The same quantizer with the quotient bf16(x / bf16(s)) (IEEE division by the
+ * scale rounded to bf16), *scale_out = s unchanged: the reference's eager
+ * expression clamp(value / scale, +-448).to(float8_e4m3fn) as torch evaluates
+ * it on the GPU, where a bf16 tensor divided by a 0-dim fp32 tensor computes
+ * in bf16 and casts the divisor to bf16 (measured on MI355X).  The reference
+ * takes this form for its FP8 weight conversions (FL/inference/fp8.py:259-263,
+ * :107-113) and for activations when its Triton kernels are not enabled
+ * (FL/inference/fused_kernels.py:771-795); h3q_quant_tensor_e4m3 is the form
+ * of its Triton kernels (:230-247, fp32 divisor).
+ */
+int h3q_quant_tensor_e4m3_bf16_divisor(const void* x, int64_t rows, int64_t cols, int64_t ldx,
+                                       const float* static_scale, float* partial, void* codes, int64_t ldq,
+                                       float* scale_out, void* stream);
+
+/*
+ * Per-(batch, head) e4m3fn quantization of attention operands:
+ *   x: contiguous bf16 [batch, seq, heads, head_dim]
+ *   scales[b, h] = max(amax_{s,d}(|x[b, s, h, d]|) * RN(1/448), 1e-12)   (fp32 [batch, heads])
+ *   codes[b, s, h, d] = e4m3(clamp(x / scales[b, h], +-448))   (fp32 quotient, no bf16 intermediate)
+ * Replaces quantize_fp8_e4m3_per_head (FL/inference/fused_kernels.py:823-877;
+ * Triton :175-227, :250-273), called for the FP8 attention inputs at
+ * FL/streaming/attention_hook.py:1018-1043 and FL/streaming/cache.py:838-853.
+ * `partial` is caller workspace of
+ * h3q_quant_per_head_workspace_floats(batch, seq, heads, head_dim) floats.
+ * batch == 0 or heads == 0 is a no-op; seq == 0 or head_dim == 0 is
+ * H3Q_ERR_INVALID (an empty reduction, as torch's amax); heads <= 4096.
+ * head_dim % 8 == 0 with a 16-byte aligned x and 8-byte aligned codes takes
+ * the vector path; anything else runs element by element.  Two kernels:
+ * per-chunk head maxima, then fold + quantize.
+ */
+int64_t h3q_quant_per_head_workspace_floats(int64_t batch, int64_t seq, int64_t heads, int64_t head_dim);
+int h3q_quant_per_head_e4m3(const void* x, int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                            float* partial, void* codes, float* scales, void* stream);
 
 /*
  * Scaled GEMM with fused epilogue:

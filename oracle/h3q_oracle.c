@@ -17,6 +17,9 @@
  *   orc_quant_tensor_e4m3      FL/inference/fused_kernels.py:771-796 (eager) and
  *                              :140-172,230-247 (Triton: bf16 intermediate);
  *                              FL/inference/fp8.py:259-263 (weights)
+ *   orc_quant_per_head_e4m3    FL/inference/fused_kernels.py:823-877 (eager :826-834;
+ *                              Triton :175-227, :250-273): per-(batch, head) scale,
+ *                              fp32 quotient
  *   orc_gemm_i8_i32            exact int32 accumulators of cutlass_scaled_mm
  *                              (H3/inference/w8a8.py:179-186)
  *   orc_gemm_e4m3_f64          exact real value of an e4m3 x e4m3 dot product
@@ -116,6 +119,20 @@ static const float kE4M3Max = 448.0f;
 static const float kInt8Max = 127.0f;
 static const float kScaleFloor = 1.0e-12f;   /* torch.clamp(min=1.0e-12) on fp32 */
 
+/* Scale from an absolute maximum, as the reference's expression
+ * clamp(amax.float() / L, min=1e-12) evaluates on the GPU: PyTorch's device
+ * kernel for a tensor divided by a Python scalar multiplies by the binary32
+ * reciprocal of the scalar, and the reference's Triton finalize kernels write
+ * the same product, maximum * (1.0 / LIMIT) (FL/inference/fused_kernels.py:171,
+ * 226).  So s = RN(amax * RN(1/L)), floored at 1e-12; a true division
+ * amax / L (torch on the CPU) differs in the last bit for about half of the
+ * bf16 amax values at L = 448. */
+static float amax_scale(float amax, float limit) {
+    const float r = 1.0f / limit;
+    const float s = amax * r;
+    return s < kScaleFloor ? kScaleFloor : s;
+}
+
 static float row_amax(const uint16_t* x, int64_t k) {
     float amax = 0.0f;
     for (int64_t j = 0; j < k; ++j) {
@@ -126,7 +143,7 @@ static float row_amax(const uint16_t* x, int64_t k) {
 }
 
 /* H3/inference/w8a8.py:57-63:
- *   scale = clamp(amax_row(|W|).float() / 127, min=1e-12)
+ *   scale = clamp(amax_row(|W|).float() / 127, min=1e-12)   (amax_scale)
  *   q     = int8(clamp(round_half_even(float(W) / scale), -127, 127))
  * bf16 [rows,K] / fp32 [rows,1] promotes to fp32, so the quotient is one
  * correctly rounded binary32 division. */
@@ -134,8 +151,7 @@ ORC_API void orc_quant_rows_int8_div(const uint16_t* x, int64_t rows, int64_t k,
                                      int8_t* q, int64_t ldq, float* scales) {
     for (int64_t i = 0; i < rows; ++i) {
         const uint16_t* xr = x + i * ldx;
-        float s = row_amax(xr, k) / kInt8Max;
-        if (s < kScaleFloor) s = kScaleFloor;
+        const float s = amax_scale(row_amax(xr, k), kInt8Max);
         scales[i] = s;
         for (int64_t j = 0; j < k; ++j) {
             float v = nearbyintf(orc_bf16_to_f32(xr[j]) / s);
@@ -147,19 +163,49 @@ ORC_API void orc_quant_rows_int8_div(const uint16_t* x, int64_t rows, int64_t k,
 }
 
 /* Per-row e4m3fn with an fp32 quotient:
- *   scale = clamp(amax_row / 448, min=1e-12);  q = e4m3(clamp(float(x)/scale, +-448)) */
+ *   scale = clamp(amax_row / 448, min=1e-12) (amax_scale);  q = e4m3(clamp(float(x)/scale, +-448)) */
 ORC_API void orc_quant_rows_e4m3_div(const uint16_t* x, int64_t rows, int64_t k, int64_t ldx,
                                      uint8_t* q, int64_t ldq, float* scales) {
     for (int64_t i = 0; i < rows; ++i) {
         const uint16_t* xr = x + i * ldx;
-        float s = row_amax(xr, k) / kE4M3Max;
-        if (s < kScaleFloor) s = kScaleFloor;
+        const float s = amax_scale(row_amax(xr, k), kE4M3Max);
         scales[i] = s;
         for (int64_t j = 0; j < k; ++j) {
             float v = orc_bf16_to_f32(xr[j]) / s;
             if (v < -kE4M3Max) v = -kE4M3Max;
             if (v > kE4M3Max) v = kE4M3Max;
             q[i * ldq + j] = orc_f32_to_e4m3(v);
+        }
+    }
+}
+
+/* Per-(batch, head) e4m3fn of x [batch, seq, heads, head_dim]
+ * (FL/inference/fused_kernels.py:823-877):
+ *   scale[b, h] = clamp(amax_{s,d}(|x|).float() / 448, min=1e-12)   (amax_scale)
+ *   q = e4m3(clamp(float(x) / scale[b, h], +-448))
+ * bf16 [B,S,H,D] / fp32 [B,1,H,1] promotes to fp32: one correctly rounded
+ * binary32 division, no bf16 intermediate (the Triton kernel's div_rn). */
+ORC_API void orc_quant_per_head_e4m3(const uint16_t* x, int64_t batch, int64_t seq, int64_t heads,
+                                     int64_t head_dim, uint8_t* q, float* scales) {
+    const int64_t row = heads * head_dim;
+    for (int64_t b = 0; b < batch; ++b) {
+        for (int64_t h = 0; h < heads; ++h) {
+            float amax = 0.0f;
+            for (int64_t t = 0; t < seq; ++t) {
+                float a = row_amax(x + (b * seq + t) * row + h * head_dim, head_dim);
+                if (a > amax || isnan(a)) amax = a;
+            }
+            const float s = amax_scale(amax, kE4M3Max);
+            scales[b * heads + h] = s;
+            for (int64_t t = 0; t < seq; ++t) {
+                const int64_t off = (b * seq + t) * row + h * head_dim;
+                for (int64_t d = 0; d < head_dim; ++d) {
+                    float v = orc_bf16_to_f32(x[off + d]) / s;
+                    if (v < -kE4M3Max) v = -kE4M3Max;
+                    if (v > kE4M3Max) v = kE4M3Max;
+                    q[off + d] = orc_f32_to_e4m3(v);
+                }
+            }
         }
     }
 }
@@ -188,14 +234,17 @@ ORC_API void orc_quant_rows_int8_rcp(const uint16_t* x, int64_t rows, int64_t k,
 }
 
 /* Per-tensor e4m3fn (FL/inference/fused_kernels.py:771-796, fp8.py:259-263):
- *   scale = clamp(amax_all.float() / 448, min=1e-12)      (0-dim fp32)
- *   q = e4m3(clamp(bf16(float(x) / scale), +-448))
+ *   scale = clamp(amax_all.float() / 448, min=1e-12)      (0-dim fp32, amax_scale)
+ *   q = e4m3(clamp(bf16(float(x) / d), +-448))
  * A bf16 tensor divided by a 0-dim fp32 tensor yields bf16, so the binary32
- * quotient is rounded to bf16 before the e4m3 cast (the Triton kernel's
- * _round_bf16(div_rn(x, s))).  static_scale (nullable) replaces the dynamic
- * scale as in quantize_fp8_e4m3(value, scale). */
+ * quotient is rounded to bf16 before the e4m3 cast.  The divisor d is the
+ * fp32 scale in the reference's Triton kernel (_round_bf16(div_rn(x, s)),
+ * :230-247) and in torch on the CPU; torch on the GPU computes in bf16 and
+ * casts the divisor, d = bf16(scale) (bf16_divisor != 0; the eager path of
+ * the reference on its device, e.g. its weight conversions).  static_scale
+ * (nullable) replaces the dynamic scale as in quantize_fp8_e4m3(value, scale). */
 ORC_API void orc_quant_tensor_e4m3(const uint16_t* x, int64_t rows, int64_t k, int64_t ldx,
-                                   const float* static_scale, uint8_t* q, int64_t ldq,
+                                   const float* static_scale, int bf16_divisor, uint8_t* q, int64_t ldq,
                                    float* scale_out) {
     float s;
     if (static_scale) {
@@ -206,13 +255,13 @@ ORC_API void orc_quant_tensor_e4m3(const uint16_t* x, int64_t rows, int64_t k, i
             float a = row_amax(x + i * ldx, k);
             if (a > amax || isnan(a)) amax = a;
         }
-        s = amax / kE4M3Max;
-        if (s < kScaleFloor) s = kScaleFloor;
+        s = amax_scale(amax, kE4M3Max);
     }
     *scale_out = s;
+    const float d = bf16_divisor ? orc_bf16_to_f32(orc_f32_to_bf16(s)) : s;
     for (int64_t i = 0; i < rows; ++i) {
         for (int64_t j = 0; j < k; ++j) {
-            float v = orc_bf16_to_f32(orc_f32_to_bf16(orc_bf16_to_f32(x[i * ldx + j]) / s));
+            float v = orc_bf16_to_f32(orc_f32_to_bf16(orc_bf16_to_f32(x[i * ldx + j]) / d));
             if (v < -kE4M3Max) v = -kE4M3Max;
             if (v > kE4M3Max) v = kE4M3Max;
             q[i * ldq + j] = orc_f32_to_e4m3(v);

@@ -13,12 +13,15 @@ Parity pins (each checked in ``tests/test_oracle_pins.py``):
 * ``f32_to_bf16`` / ``f32_to_e4m3`` / ``e4m3_to_f32``: against torch's casts
   over every bf16 bit pattern and a random binary32 sample.
 * ``quant_rows(..., 'int8', 'div')``: against the reference expression of
-  ``H3/inference/w8a8.py:57-63`` evaluated by torch on CPU, plus closed-form
+  ``H3/inference/w8a8.py:57-63`` evaluated by torch (on the GPU, and on the
+  CPU with the device's scalar division), plus closed-form
   special cases (zero row, argmax -> +-127, ties to even).
 * ``quant_rows(..., 'e4m3', 'div')``: against the same expression with
   127 -> 448 and torch's e4m3fn cast; special cases.
 * ``quant_tensor_e4m3``: against ``FL/inference/fused_kernels.py:771-796``'s
   eager expression evaluated by torch (bf16 intermediate), special cases.
+* ``quant_per_head_e4m3``: against ``FL/inference/fused_kernels.py:826-834``'s
+  eager expression evaluated by torch (fp32 quotient), special cases.
 * ``quant_rows(..., 'int8', 'rcp')``: vLLM semantics (third-party, absent):
   pinned only by invariants -- parity unpinned against vLLM itself.
 * ``gemm_i8_i32``: against ``torch._int_mm`` and brute force.
@@ -63,7 +66,9 @@ def _load() -> ctypes.CDLL:
         fn.restype = None
         fn.argtypes = [_p, _i64, _i64, _i64, _p, _i64, _p]
     lib.orc_quant_tensor_e4m3.restype = None
-    lib.orc_quant_tensor_e4m3.argtypes = [_p, _i64, _i64, _i64, _p, _p, _i64, _p]
+    lib.orc_quant_tensor_e4m3.argtypes = [_p, _i64, _i64, _i64, _p, ctypes.c_int, _p, _i64, _p]
+    lib.orc_quant_per_head_e4m3.restype = None
+    lib.orc_quant_per_head_e4m3.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _p]
     lib.orc_gemm_i8_i32.restype = None
     lib.orc_gemm_i8_i32.argtypes = [_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64]
     lib.orc_gemm_e4m3_f64.restype = None
@@ -159,8 +164,10 @@ def quant_rows(x_bits: np.ndarray, fmt: str, rounding: str = "div") -> tuple[np.
     return codes, scales
 
 
-def quant_tensor_e4m3(x_bits: np.ndarray, static_scale: float | None = None) -> tuple[np.ndarray, np.float32]:
-    """Per-tensor e4m3fn with the bf16 intermediate (FL/inference/fused_kernels.py:771-796)."""
+def quant_tensor_e4m3(x_bits: np.ndarray, static_scale: float | None = None,
+                      bf16_divisor: bool = False) -> tuple[np.ndarray, np.float32]:
+    """Per-tensor e4m3fn with the bf16 intermediate (FL/inference/fused_kernels.py:771-796);
+    ``bf16_divisor``: divide by bf16(scale), as torch's eager expression on the GPU."""
     lib = _load()
     x = np.ascontiguousarray(x_bits, dtype=np.uint16)
     if x.ndim == 1:
@@ -169,8 +176,22 @@ def quant_tensor_e4m3(x_bits: np.ndarray, static_scale: float | None = None) -> 
     codes = np.empty((rows, k), dtype=np.uint8)
     scale = np.zeros(1, dtype=np.float32)
     st = None if static_scale is None else np.array([static_scale], dtype=np.float32)
-    lib.orc_quant_tensor_e4m3(_ptr(x), rows, k, k, _ptr(st), _ptr(codes), k, _ptr(scale))
+    lib.orc_quant_tensor_e4m3(_ptr(x), rows, k, k, _ptr(st), int(bf16_divisor), _ptr(codes), k, _ptr(scale))
     return codes.reshape(np.shape(x_bits)), scale[0]
+
+
+def quant_per_head_e4m3(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Per-(batch, head) e4m3fn of bf16 bits [B, S, H, D] (FL/inference/fused_kernels.py:823-877):
+    (codes [B, S, H, D] uint8, scales [B, H] fp32)."""
+    lib = _load()
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    if x.ndim != 4:
+        raise ValueError(f"expected [B, S, H, D], got shape {x.shape}")
+    b, s, h, d = x.shape
+    codes = np.empty(x.shape, dtype=np.uint8)
+    scales = np.zeros((b, h), dtype=np.float32)
+    lib.orc_quant_per_head_e4m3(_ptr(x), b, s, h, d, _ptr(codes), _ptr(scales))
+    return codes, scales
 
 
 # --------------------------------------------------------------------- GEMMs

@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256) void tensor_amax_kernel(const uint16_t* __rest
 // One element of the per-tensor quantizer: e4m3(clamp(bf16(x / s), +-448)).
 struct TensorQuant {
     float s, r;
-    bool exact_div;  // static scale: plain IEEE division
+    bool exact_div;  // static scale or bf16 divisor: IEEE division
     __device__ __forceinline__ float value(float f) const {
         float qv = exact_div ? __fdiv_rn(f, s) : copysignf(div_rn(f, s, r), f);
         return __builtin_amdgcn_fmed3f(round_to_bf16(qv), -kE4M3Max, kE4M3Max);
@@ -207,12 +207,14 @@ struct TensorQuant {
 
 // Pass 2: every workgroup folds the partial maxima (or reads the static
 // scale), then quantizes its band of rows.
+// bf16_divisor: divide by bf16(s) (IEEE) instead of s, keeping s as the
+// returned scale.
 __global__ __launch_bounds__(256) void tensor_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                            int64_t rows, int64_t k, int64_t rows_per_block,
                                                            const float* __restrict__ partial, int nparts,
                                                            const float* __restrict__ static_scale,
-                                                           uint8_t* __restrict__ q, int64_t ldq,
-                                                           float* __restrict__ scale_out) {
+                                                           int bf16_divisor, uint8_t* __restrict__ q,
+                                                           int64_t ldq, float* __restrict__ scale_out) {
     __shared__ float red[4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     TensorQuant tq;
@@ -226,11 +228,15 @@ __global__ __launch_bounds__(256) void tensor_quant_kernel(const uint16_t* __res
         if (lane == 0) red[wave] = a;
         __syncthreads();
         a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        tq.s = row_scale(a, kE4M3Max);
+        tq.s = amax_scale(a, kE4M3Recip);
         tq.exact_div = false;
     }
-    tq.r = 1.0f / tq.s;
     if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = tq.s;
+    if (bf16_divisor) {
+        tq.s = round_to_bf16(tq.s);
+        tq.exact_div = true;
+    }
+    tq.r = 1.0f / tq.s;
     const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
     const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
     const bool vec = (k % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && ((uintptr_t)x % 16 == 0) &&
@@ -265,8 +271,8 @@ int64_t tensor_quant_parts(int64_t rows, int64_t k) {
 }
 
 hipError_t launch_quant_tensor_e4m3(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k,
-                                    const float* static_scale, float* partial, uint8_t* q, int64_t ldq,
-                                    float* scale_out, hipStream_t st) {
+                                    const float* static_scale, bool bf16_divisor, float* partial, uint8_t* q,
+                                    int64_t ldq, float* scale_out, hipStream_t st) {
     const int64_t parts = tensor_quant_parts(rows, k);
     const int64_t rpb = (rows + parts - 1) / parts;
     const int64_t blocks = (rows + rpb - 1) / rpb;
@@ -277,7 +283,7 @@ hipError_t launch_quant_tensor_e4m3(const uint16_t* x, int64_t ldx, int64_t rows
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(tensor_quant_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, ldx, rows, k, rpb,
-                       (const float*)partial, (int)blocks, static_scale, q, ldq, scale_out);
+                       (const float*)partial, (int)blocks, static_scale, (int)bf16_divisor, q, ldq, scale_out);
     return hipGetLastError();
 }
 

@@ -191,19 +191,61 @@ __attribute__((visibility("default"))) int64_t h3q_quant_tensor_workspace_floats
     return h3q::tensor_quant_parts(rows, cols);
 }
 
+static int quant_tensor_e4m3(const char* who, const void* x, int64_t rows, int64_t cols, int64_t ldx,
+                             const float* static_scale, bool bf16_divisor, float* partial, void* codes, int64_t ldq,
+                             float* scale_out, void* stream) {
+    if (rows <= 0 || cols <= 0) return fail(H3Q_ERR_INVALID, "%s: empty tensor has no amax", who);
+    if (ldx < cols || ldq < cols) return fail(H3Q_ERR_INVALID, "%s: leading dimension below cols", who);
+    if (!x || !codes || !scale_out || (!static_scale && !partial))
+        return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
+    return check_launch(h3q::launch_quant_tensor_e4m3((const uint16_t*)x, ldx, rows, cols, static_scale, bf16_divisor,
+                                                      partial, (uint8_t*)codes, ldq, scale_out, (hipStream_t)stream),
+                        who);
+}
+
 __attribute__((visibility("default"))) int h3q_quant_tensor_e4m3(const void* x, int64_t rows, int64_t cols,
                                                                  int64_t ldx, const float* static_scale,
                                                                  float* partial, void* codes, int64_t ldq,
                                                                  float* scale_out, void* stream) {
-    if (rows <= 0 || cols <= 0)
-        return fail(H3Q_ERR_INVALID, "h3q_quant_tensor_e4m3: empty tensor has no amax");
-    if (ldx < cols || ldq < cols)
-        return fail(H3Q_ERR_INVALID, "h3q_quant_tensor_e4m3: leading dimension below cols");
-    if (!x || !codes || !scale_out || (!static_scale && !partial))
-        return fail(H3Q_ERR_INVALID, "h3q_quant_tensor_e4m3: null pointer");
-    return check_launch(h3q::launch_quant_tensor_e4m3((const uint16_t*)x, ldx, rows, cols, static_scale, partial,
-                                                      (uint8_t*)codes, ldq, scale_out, (hipStream_t)stream),
-                        "h3q_quant_tensor_e4m3");
+    return quant_tensor_e4m3("h3q_quant_tensor_e4m3", x, rows, cols, ldx, static_scale, false, partial, codes, ldq,
+                             scale_out, stream);
+}
+
+__attribute__((visibility("default"))) int h3q_quant_tensor_e4m3_bf16_divisor(const void* x, int64_t rows,
+                                                                              int64_t cols, int64_t ldx,
+                                                                              const float* static_scale,
+                                                                              float* partial, void* codes,
+                                                                              int64_t ldq, float* scale_out,
+                                                                              void* stream) {
+    return quant_tensor_e4m3("h3q_quant_tensor_e4m3_bf16_divisor", x, rows, cols, ldx, static_scale, true, partial,
+                             codes, ldq, scale_out, stream);
+}
+
+__attribute__((visibility("default"))) int64_t h3q_quant_per_head_workspace_floats(int64_t batch, int64_t seq,
+                                                                                   int64_t heads, int64_t head_dim) {
+    if (batch <= 0 || seq <= 0 || heads <= 0 || head_dim <= 0 || heads > h3q::kMaxHeads) return 1;
+    return h3q::per_head_quant_parts(batch, seq, heads, head_dim);
+}
+
+__attribute__((visibility("default"))) int h3q_quant_per_head_e4m3(const void* x, int64_t batch, int64_t seq,
+                                                                   int64_t heads, int64_t head_dim, float* partial,
+                                                                   void* codes, float* scales, void* stream) {
+    const char* who = "h3q_quant_per_head_e4m3";
+    if (batch < 0 || seq < 0 || heads < 0 || head_dim < 0) return fail(H3Q_ERR_INVALID, "%s: negative shape", who);
+    if (batch == 0 || heads == 0) return H3Q_OK;  // no (batch, head) pair: nothing to reduce or write
+    if (seq == 0 || head_dim == 0)
+        return fail(H3Q_ERR_INVALID, "%s: empty (seq, head_dim) reduction has no amax", who);
+    if (heads > h3q::kMaxHeads)
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: heads=%lld above %lld", who, (long long)heads,
+                    (long long)h3q::kMaxHeads);
+    if (heads * head_dim >= (int64_t(1) << 30) || batch * heads >= (int64_t(1) << 30))
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: row or batch x heads above 2^30", who);
+    if (!x || !partial || !codes || !scales) return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
+    if (!aligned(x, 2) || !aligned(scales, 4) || !aligned(partial, 4))
+        return fail(H3Q_ERR_INVALID, "%s: misaligned pointer", who);
+    return check_launch(h3q::launch_quant_per_head_e4m3((const uint16_t*)x, batch, seq, heads, head_dim, partial,
+                                                        (uint8_t*)codes, scales, (hipStream_t)stream),
+                        who);
 }
 
 static int check_gemm_operands(const char* who, const void* a, int64_t lda, const void* b, int64_t ldb, int64_t m,

@@ -18,8 +18,17 @@ hipError_t launch_quant_rows_tiled(const uint16_t* x, int64_t ldx, int64_t rows,
 int64_t tensor_quant_parts(int64_t rows, int64_t k);
 
 hipError_t launch_quant_tensor_e4m3(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k,
-                                    const float* static_scale, float* partial, uint8_t* q, int64_t ldq,
-                                    float* scale_out, hipStream_t st);
+                                    const float* static_scale, bool bf16_divisor, float* partial, uint8_t* q,
+                                    int64_t ldq, float* scale_out, hipStream_t st);
+
+// Per-(batch, head) e4m3fn quantization of a contiguous [batch, seq, heads,
+// head_dim] bf16 tensor: codes of the same shape, scales [batch, heads].
+// partial holds per_head_quant_parts(...) floats.
+constexpr int64_t kMaxHeads = 4096;
+int64_t per_head_quant_parts(int64_t batch, int64_t seq, int64_t heads, int64_t head_dim);
+hipError_t launch_quant_per_head_e4m3(const uint16_t* x, int64_t batch, int64_t seq, int64_t heads,
+                                      int64_t head_dim, float* partial, uint8_t* q, float* scales,
+                                      hipStream_t st);
 
 // Operand kinds of the MFMA GEMM.
 enum OpKind : int { kOpE4M3 = 0, kOpInt8 = 1, kOpBF16 = 2 };

@@ -20,12 +20,16 @@ constexpr float kE4M3Max = 448.0f;
 constexpr float kInt8Max = 127.0f;
 constexpr float kScaleFloor = 1.0e-12f;
 
+// The reciprocals of the limits, rounded to binary32 (RN(1/448), RN(1/127)).
+constexpr float kE4M3Recip = 1.0f / 448.0f;
+constexpr float kInt8Recip = 1.0f / 127.0f;
+
 // Correctly rounded binary32 quotient x / s from r = RN(1 / s), one residual
 // correction (Markstein's division scheme):
 //   q0 = RN(x * r)               within one ulp of x / s
 //   e  = x - q0 * s              exact, computed by one fused multiply-add
 //   q1 = RN(q0 + e * r)          = RN(x / s)
-// Every divisor a row quantizer uses is max(amax / c, 1e-12) for a bf16 amax
+// Every divisor a quantizer uses is amax_scale(amax, RN(1/c)) for a bf16 amax
 // and c in {127, 448}, and every dividend is a bf16 value with |x| <= amax;
 // the test suite checks q1 == x / s bit for bit over that whole set.
 H3Q_HD float div_rn(float x, float s, float r) {
@@ -34,10 +38,19 @@ H3Q_HD float div_rn(float x, float s, float r) {
     return fmaf(e, r, q0);
 }
 
-// Row scale from the row's absolute maximum (H3/inference/w8a8.py:58-61,
-// with limit 127 for int8 codes and 448 for e4m3fn codes).
-H3Q_HD float row_scale(float amax, float limit) {
-    float s = amax / limit;
+// Scale of a dynamic quantizer from its absolute maximum:
+//   s = max(RN(amax * RN(1/limit)), 1e-12)
+// The reference writes torch.clamp(amax.float() / limit, min=1.0e-12)
+// (H3/inference/w8a8.py:58-61 with limit 127; FL/inference/fused_kernels.py:
+// 791-794, 826-829 and fp8.py:259-262 with 448) and evaluates it on the GPU,
+// where PyTorch's kernel for a tensor divided by a Python scalar multiplies by
+// the binary32 reciprocal of the scalar: measured on MI355X, bit-identical to
+// this form for every bf16 amax, while a true division differs for 1,488 (127)
+// and 17,468 (448) of the 32,640 finite values.  The reference's Triton
+// finalize kernels compute the same product, maximum * (1.0 / LIMIT)
+// (FL/inference/fused_kernels.py:155-172, 209-227).
+H3Q_HD float amax_scale(float amax, float recip) {
+    float s = amax * recip;
     return s < kScaleFloor ? kScaleFloor : s;
 }
 

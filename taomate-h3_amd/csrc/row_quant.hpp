@@ -37,7 +37,7 @@ struct RowQuant {
             s = amax / kInt8Max;
             r = (amax == 0.0f) ? 0.0f : kInt8Max / amax;
         } else {
-            s = row_scale(amax, FMT == kFmtE4M3 ? kE4M3Max : kInt8Max);
+            s = amax_scale(amax, FMT == kFmtE4M3 ? kE4M3Recip : kInt8Recip);
             r = 1.0f / s;
         }
     }

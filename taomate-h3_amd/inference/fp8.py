@@ -79,8 +79,10 @@ def resolve_h3_dynamic_fp8_policy(linear_names: list[str], *, policy: str | None
 
 
 def quantize_weight_fp8_tensor(weight: Any) -> tuple[Any, Any]:
-    """Per-tensor e4m3fn weight codes and 0-dim fp32 scale (FL/inference/fp8.py:259-263)."""
-    return ops.quant_tensor_e4m3(weight.detach().contiguous())
+    """Per-tensor e4m3fn weight codes and 0-dim fp32 scale (FL/inference/fp8.py:259-263,
+    :107-113): the eager expression as torch evaluates it on the GPU, so the
+    quotient's divisor is the scale rounded to bf16."""
+    return ops.quant_tensor_e4m3(weight.detach().contiguous(), bf16_divisor=True)
 
 
 def quantize_weight_fp8_rows(weight: Any) -> tuple[Any, Any]:

@@ -1,18 +1,26 @@
-"""FP8 quantizers of FL/inference/fused_kernels.py:771-820 and the
+"""FP8 quantizers of FL/inference/fused_kernels.py:771-877 and the
 RMSNorm/AdaLN producers of H3/inference/fused_kernels.py:700-773 on gfx950.
 
 Same names, arguments and results as the reference; the Triton kernels
 (amax partial/finalize + quantize, three launches) are replaced by
 ``h3q_quant_tensor_e4m3`` (two launches: partial maxima, then a pass that
-folds them and quantizes).  Codes are bit-identical to the reference's eager
-expression ``clamp(value / scale, +-448).to(float8_e4m3fn)``, whose quotient
-is a bf16 tensor (bf16 divided by a 0-dim fp32 tensor), i.e. the binary32
-quotient rounded to bf16 before the e4m3fn cast.
+folds them and quantizes).  The quotient is a bf16 tensor (bf16 divided by a
+0-dim fp32 tensor), i.e. the binary32 quotient rounded to bf16 before the
+e4m3fn cast.  Its divisor follows the reference's mode: after
+``enable_h3_inference_fused_kernels()`` the fp32 scale (the Triton kernel's
+``_round_bf16(div_rn(value, scale))``), otherwise the scale rounded to bf16
+(the eager ``clamp(value / scale, +-448)`` as torch computes it on the GPU).
 
-``quantize_fp8_e4m3_rowwise`` is the per-token (per-row) quantizer of the
-per-token x per-channel FP8 W8A8 linear: fp32 quotient, scale
-``max(amax_row / 448, 1e-12)``.  There is no bf16 fallback: inputs must be
-bf16 tensors on a ROCm device.
+Dynamic scales are ``max(amax * RN(1/448), 1e-12)``: the reference's
+``clamp(amax / 448, min=1e-12)`` as torch evaluates it on the GPU (a tensor
+divided by a Python scalar is a multiply by the binary32 reciprocal) and as its
+Triton finalize kernels write it.
+
+``quantize_fp8_e4m3_per_head`` (``h3q_quant_per_head_e4m3``) keeps the
+reference's per-(batch, head) scales and fp32 quotient for the FP8 attention
+operands.  ``quantize_fp8_e4m3_rowwise`` is the per-token (per-row) quantizer
+of the per-token x per-channel FP8 W8A8 linear: fp32 quotient.  There is no
+bf16 fallback: inputs must be bf16 tensors on a ROCm device.
 
 ``fused_rms_norm_modulate`` and ``fused_residual_gate_rms_norm_modulate``
 keep the reference's names, arguments, results and index check.  Their
@@ -34,6 +42,26 @@ import torch
 from .. import ops
 
 FP8_MAX = 448.0
+_ENABLED = False
+
+
+def enable_h3_inference_fused_kernels() -> None:
+    """FL/inference/fused_kernels.py:14-18: select the reference's Triton forms.
+    The one observable difference on this path is the per-tensor FP8 quotient:
+    enabled, the fp32 scale divides (the Triton kernel); disabled, the divisor
+    is the scale rounded to bf16, as the reference's eager expression
+    evaluates on the GPU.  The per-head quantizer is the same either way."""
+    global _ENABLED
+    _ENABLED = True
+
+
+def enable_h3_sol_engine_fusions() -> None:
+    """FL/inference/fused_kernels.py:21-26 (implies the fused kernels)."""
+    enable_h3_inference_fused_kernels()
+
+
+def h3_inference_fused_kernels_enabled() -> bool:
+    return _ENABLED
 
 
 def _as_bf16(value: torch.Tensor, name: str) -> torch.Tensor:
@@ -47,15 +75,24 @@ def quantize_fp8_e4m3(value: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     (FL/inference/fused_kernels.py:771-785)."""
     _as_bf16(value, "quantize_fp8_e4m3")
     scale = scale.to(device=value.device, dtype=torch.float32)
-    codes, _ = ops.quant_tensor_e4m3(value.contiguous(), scale.reshape(()))
+    codes, _ = ops.quant_tensor_e4m3(value.contiguous(), scale.reshape(()), bf16_divisor=not _ENABLED)
     return codes
 
 
 def quantize_fp8_e4m3_dynamic(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Dynamic per-tensor e4m3fn: (codes, 0-dim fp32 scale ``max(amax/448, 1e-12)``)
+    """Dynamic per-tensor e4m3fn: (codes, 0-dim fp32 scale ``max(amax * RN(1/448), 1e-12)``)
     (FL/inference/fused_kernels.py:788-820)."""
     _as_bf16(value, "quantize_fp8_e4m3_dynamic")
-    return ops.quant_tensor_e4m3(value.contiguous())
+    return ops.quant_tensor_e4m3(value.contiguous(), bf16_divisor=not _ENABLED)
+
+
+def quantize_fp8_e4m3_per_head(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-(batch, head) e4m3fn of attention operands ``value [B, S, H, D]``
+    (FL/inference/fused_kernels.py:823-877): (codes [B, S, H, D], fp32 scales
+    [B, H]), the scales being the descales FlashAttention-3 takes
+    (FL/streaming/attention_hook.py:1018-1043, FL/streaming/cache.py:838-853)."""
+    _as_bf16(value, "quantize_fp8_e4m3_per_head")
+    return ops.quant_per_head_e4m3(value)
 
 
 def quantize_fp8_e4m3_rowwise(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -164,6 +201,8 @@ def fused_residual_gate_rms_norm_modulate_w8a8(residual: torch.Tensor, branch: t
     return hidden.reshape(residual.shape), QuantizedActivations(codes, scales, tuple(residual.shape), fmt, dense)
 
 
-__all__ = ["FP8_MAX", "QuantizedActivations", "as_dense", "fused_residual_gate_rms_norm_modulate",
+__all__ = ["FP8_MAX", "QuantizedActivations", "as_dense", "enable_h3_inference_fused_kernels",
+           "enable_h3_sol_engine_fusions", "fused_residual_gate_rms_norm_modulate", "h3_inference_fused_kernels_enabled",
            "fused_residual_gate_rms_norm_modulate_w8a8", "fused_rms_norm_modulate", "fused_rms_norm_modulate_w8a8",
-           "quantize_fp8_e4m3", "quantize_fp8_e4m3_dynamic", "quantize_fp8_e4m3_rowwise"]
+           "quantize_fp8_e4m3", "quantize_fp8_e4m3_dynamic", "quantize_fp8_e4m3_per_head",
+           "quantize_fp8_e4m3_rowwise"]

@@ -238,8 +238,11 @@ def quant_rows_tiled(x: torch.Tensor, fmt: int, rounding: int = ROUND_DIV, *, co
 
 def quant_tensor_e4m3(x: torch.Tensor, static_scale: torch.Tensor | None = None, *,
                       codes: torch.Tensor | None = None, scale: torch.Tensor | None = None,
-                      workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """Per-tensor e4m3fn with the bf16 intermediate; returns (codes, 0-dim fp32 scale)."""
+                      workspace: torch.Tensor | None = None,
+                      bf16_divisor: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-tensor e4m3fn with the bf16 intermediate; returns (codes, 0-dim fp32 scale).
+    ``bf16_divisor``: divide by the scale rounded to bf16 (the reference's
+    eager expression on the GPU) instead of the fp32 scale (its Triton kernel)."""
     _require_gpu("quant_tensor_e4m3", x, static_scale, codes, scale, workspace)
     if x.dtype != torch.bfloat16:
         raise TypeError(f"quant_tensor_e4m3: expected bfloat16 input, got {x.dtype}")
@@ -260,9 +263,38 @@ def quant_tensor_e4m3(x: torch.Tensor, static_scale: torch.Tensor | None = None,
     elif workspace is None:
         n = int(_lib.lib().h3q_quant_tensor_workspace_floats(rows, cols))
         workspace = torch.empty(n, device=x.device, dtype=torch.float32)
-    _lib.call("h3q_quant_tensor_e4m3", _ptr(x2), rows, cols, x2.stride(0), _ptr(static_scale), _ptr(workspace),
+    _lib.call("h3q_quant_tensor_e4m3_bf16_divisor" if bf16_divisor else "h3q_quant_tensor_e4m3", _ptr(x2), rows,
+              cols, x2.stride(0), _ptr(static_scale), _ptr(workspace),
               _ptr(c2), c2.stride(0), _ptr(scale), _stream(x))
     return codes, scale
+
+
+def quant_per_head_e4m3(x: torch.Tensor, *, codes: torch.Tensor | None = None, scales: torch.Tensor | None = None,
+                        workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-(batch, head) e4m3fn of a bf16 ``x [B, S, H, D]``: (codes [B, S, H, D]
+    float8_e4m3fn, scales [B, H] fp32) with scale = max(amax * RN(1/448), 1e-12)
+    over (S, D) and an fp32 quotient."""
+    _require_gpu("quant_per_head_e4m3", x, codes, scales, workspace)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"quant_per_head_e4m3: expected bfloat16 input, got {x.dtype}")
+    if x.ndim != 4:
+        raise ValueError(f"quant_per_head_e4m3: expected [batch, seq, heads, head_dim], got shape {tuple(x.shape)}")
+    x = x.contiguous()
+    b, s, h, d = (int(v) for v in x.shape)
+    if codes is None:
+        codes = torch.empty(x.shape, device=x.device, dtype=torch.float8_e4m3fn)
+    if codes.shape != x.shape or codes.dtype != torch.float8_e4m3fn or not codes.is_contiguous():
+        raise ValueError("quant_per_head_e4m3: codes must be a contiguous float8_e4m3fn tensor of the input shape")
+    if scales is None:
+        scales = torch.empty((b, h), device=x.device, dtype=torch.float32)
+    if scales.numel() != b * h or scales.dtype != torch.float32 or not scales.is_contiguous():
+        raise ValueError("quant_per_head_e4m3: scales must be a contiguous fp32 tensor of batch x heads entries")
+    if workspace is None:
+        n = int(_lib.lib().h3q_quant_per_head_workspace_floats(b, s, h, d))
+        workspace = torch.empty(n, device=x.device, dtype=torch.float32)
+    _lib.call("h3q_quant_per_head_e4m3", _ptr(x), b, s, h, d, _ptr(workspace), _ptr(codes), _ptr(scales),
+              _stream(x))
+    return codes, scales
 
 
 def _scale_kind(name: str, s: torch.Tensor, count: int) -> int:

@@ -95,3 +95,28 @@ def test_norm_quant_errors_without_gpu():
     rc = lib.h3q_rms_norm_modulate_quant(None, 8200, None, None, None, 8200, None, 4, 8200, f, ctypes.c_void_p(64),
                                          8200, 1, 1, None, 8200, None, None)
     assert rc == 2 and b"above 8192" in lib.h3q_last_error()
+
+
+def test_per_head_quant_errors_without_gpu():
+    """h3q_quant_per_head_e4m3 validates its request on the host: empty
+    reductions and too many heads are refused, an empty batch is a no-op."""
+    from taomate_h3_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("library not built")
+    lib = _lib.lib()
+    p = ctypes.c_void_p(256)
+    assert lib.h3q_quant_per_head_e4m3(p, 0, 16, 4, 128, p, p, p, None) == 0
+    assert lib.h3q_quant_per_head_e4m3(p, 2, 16, 0, 128, p, p, p, None) == 0
+    rc = lib.h3q_quant_per_head_e4m3(p, 1, 0, 4, 128, p, p, p, None)
+    assert rc == 1 and b"empty" in lib.h3q_last_error()
+    rc = lib.h3q_quant_per_head_e4m3(p, 1, 8, 4097, 8, p, p, p, None)
+    assert rc == 2 and b"above 4096" in lib.h3q_last_error()
+    rc = lib.h3q_quant_per_head_e4m3(p, 1, 8, 4, 128, None, p, p, None)
+    assert rc == 1 and b"null" in lib.h3q_last_error()
+    rc = lib.h3q_quant_per_head_e4m3(p, -1, 8, 4, 128, p, p, p, None)
+    assert rc == 1 and b"negative" in lib.h3q_last_error()
+    # workspace: batch * heads * chunks, chunks <= 64 and chunks * heads <= 4096
+    assert lib.h3q_quant_per_head_workspace_floats(1, 8192, 40, 128) == 40 * 64
+    assert lib.h3q_quant_per_head_workspace_floats(2, 3, 4096, 8) == 2 * 4096
+    assert lib.h3q_quant_per_head_workspace_floats(1, 5, 3, 128) == 3 * 5

@@ -1,7 +1,8 @@
 """Exhaustive host check of the device quotient scheme in csrc/quant_math.h.
 
-Every divisor a row quantizer forms is max(amax / L, 1e-12) for a bf16 amax
-(L = 127 or 448) and every dividend is a bf16 x with |x| <= amax.  Over all
+Every divisor a quantizer forms is max(amax * RN(1/L), 1e-12) for a bf16
+amax (L = 127 or 448; amax_scale) and every dividend is a bf16 x with
+|x| <= amax.  Over all
 ~1.07e9 such pairs per L, div_rn(x, s, RN(1/s)) (three fused ops) must equal
 IEEE x / s bit for bit, except where |x / s| < 2^-70 (the residual underflows),
 where both quotients produce the same code 0.  The header is compiled with
@@ -25,11 +26,12 @@ int main(){
   int rc = 0;
   for (int lim=0; lim<2; ++lim){
     const float L = lim ? h3q::kE4M3Max : h3q::kInt8Max;
+    const float R = lim ? h3q::kE4M3Recip : h3q::kInt8Recip;
     long long bad_big = 0, bad_small = 0, total = 0;
     #pragma omp parallel for schedule(dynamic,64) reduction(+:bad_big,bad_small,total)
     for (uint32_t ah = 0; ah < 0x7F80; ++ah) {
       const float amax = bf((uint16_t)ah);
-      const float s = h3q::row_scale(amax, L);
+      const float s = h3q::amax_scale(amax, R);
       const float r = 1.0f / s;
       for (uint32_t xh = 0; xh <= ah; ++xh) {
         for (int sg = 0; sg < 2; ++sg) {

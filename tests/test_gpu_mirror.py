@@ -156,15 +156,25 @@ def test_model_level_int8_flow(oracle, device):
                                           _int8_reference(oracle, x, sources[name]))
 
 
-def test_fp8_tensor_quantizers(oracle, device):
+@pytest.mark.parametrize("fused", [False, True])
+def test_fp8_tensor_quantizers(oracle, device, monkeypatch, fused):
+    """Per-tensor quantizers in both reference modes: eager on the GPU (the
+    divisor is the scale rounded to bf16) and with the fused Triton kernels
+    enabled (fp32 divisor)."""
     fk = _mod("inference.fused_kernels")
+    monkeypatch.setattr(fk, "_ENABLED", fused)
     x = activations(333, 1040, seed=4, outlier_channels=5)
     q, s = fk.quantize_fp8_e4m3_dynamic(x.to(device))
-    rq, rs = oracle.quant_tensor_e4m3(bits16(x))
+    rq, rs = oracle.quant_tensor_e4m3(bits16(x), bf16_divisor=not fused)
     np.testing.assert_array_equal(bits8(q), rq)
     assert s.dim() == 0 and np.float32(s.item()) == rs
     q2 = fk.quantize_fp8_e4m3(x.to(device), torch.tensor(0.0123, device=device))
-    np.testing.assert_array_equal(bits8(q2), oracle.quant_tensor_e4m3(bits16(x), np.float32(0.0123))[0])
+    np.testing.assert_array_equal(bits8(q2), oracle.quant_tensor_e4m3(bits16(x), np.float32(0.0123),
+                                                                      bf16_divisor=not fused)[0])
+    # the eager expression evaluated by torch on the GPU is the unfused mode
+    ref = torch.clamp(x.to(device) / s, -448.0, 448.0).to(torch.float8_e4m3fn)
+    if not fused:
+        np.testing.assert_array_equal(bits8(ref), bits8(q))
     q3, s3 = fk.quantize_fp8_e4m3_rowwise(x.reshape(9, 37, 1040).to(device))
     rq3, rs3 = oracle.quant_rows(bits16(x), "e4m3")
     assert tuple(s3.shape) == (9, 37, 1)
@@ -210,8 +220,9 @@ def test_fp8_per_tensor_module_dispatch(oracle, device):
     receipt = fp8.quantize_h3_block_linears_dynamic_fp8_(torch, model)
     assert receipt["linear_count"] == 28 and receipt["weight_scale"] == "static_per_tensor"
     x = activations(130, 512, seed=9, outlier_channels=3)
-    rqa, rsa = oracle.quant_tensor_e4m3(bits16(x))
-    rqw, rsw = oracle.quant_tensor_e4m3(bits16(weight))
+    # eager mode (the fused kernels not enabled): bf16 divisors on the GPU
+    rqa, rsa = oracle.quant_tensor_e4m3(bits16(x), bf16_divisor=True)
+    rqw, rsw = oracle.quant_tensor_e4m3(bits16(weight), bf16_divisor=True)
     np.testing.assert_array_equal(bits8(fc2.weight), rqw)
     # row-parallel: partial output without bias, bias added after the reduction
     local = fc2.forward_local(x.to(device))
@@ -236,15 +247,14 @@ def test_fp8_calibrated_scale_then_static(oracle, device):
     fc1(xb.to(device))
     torch.cuda.synchronize()
     amax = max(float(xa.float().abs().max()), float(xb.float().abs().max()))
-    # torch evaluates tensor / 448.0 on the device as a multiply by the
-    # rounded reciprocal, so allow one binary32 ulp
-    assert np.isclose(fc1._fp8_activation_scale.item(), amax / 448.0, rtol=2.0 ** -23, atol=0)
+    # torch evaluates tensor / 448.0 on the device as a multiply by RN(1/448)
+    assert np.float32(fc1._fp8_activation_scale.item()) == np.float32(amax) * (np.float32(1.0) / np.float32(448.0))
     assert fc1._fp8_activation_calibration_remaining == 0
     xc = activations(64, 256, seed=3)
     static = np.float32(fc1._fp8_activation_scale.item() * np.float32(1.25))
     out = fc1(xc.to(device))
     torch.cuda.synchronize()
-    rqa, _ = oracle.quant_tensor_e4m3(bits16(xc), static)
+    rqa, _ = oracle.quant_tensor_e4m3(bits16(xc), static, bf16_divisor=True)
     rqw = bits8(fc1.weight)
     rsw = np.float32(fc1._fp8_weight_scale.item())
     _assert_fp8_close(oracle, bits16(out), rqa, np.array([static]), rqw, np.array([rsw]), None)

@@ -113,6 +113,21 @@ def test_tensor_e4m3_matches_oracle(ops, oracle, device, static, m, k):
     np.testing.assert_array_equal(bits8(q), rq)
 
 
+@pytest.mark.parametrize("static", [False, True])
+@pytest.mark.parametrize("m,k", [(1000, 5120), (3, 37)])
+def test_tensor_e4m3_bf16_divisor_matches_oracle(ops, oracle, device, static, m, k):
+    """The eager-on-GPU form (h3q_quant_tensor_e4m3_bf16_divisor): divisor
+    bf16(s), returned scale s."""
+    x = activations(m, k, seed=m + k + 1, outlier_channels=max(1, k // 100))
+    st = 0.0371 if static else None
+    sg = torch.tensor(st, dtype=torch.float32, device=device) if static else None
+    q, s = ops.quant_tensor_e4m3(x.to(device), sg, bf16_divisor=True)
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_tensor_e4m3(bits16(x), st, bf16_divisor=True)
+    assert np.float32(s.item()) == rs
+    np.testing.assert_array_equal(bits8(q), rq)
+
+
 def test_tensor_e4m3_3d_input(ops, oracle, device):
     x = activations(2 * 48, 256, seed=3).reshape(2, 48, 256)
     q, s = ops.quant_tensor_e4m3(x.to(device))

@@ -120,6 +120,23 @@ def test_e4m3_row_quant_closed_forms(oracle):
     assert q[0, 5] == 0x80
 
 
+def test_scale_is_the_device_reciprocal_product(oracle):
+    """The reference evaluates clamp(amax / L, min=1e-12) on the GPU, where
+    torch multiplies by RN(1/L) (the GPU suite checks that on the device).
+    Rows [amax, 0] for every finite bf16 amax: the oracle's scales equal that
+    product, and the true division (torch on the CPU) differs for many amax,
+    so the pin tells the two forms apart."""
+    vals = ALL_BF16[:0x7F80]
+    rows = np.stack([vals, np.zeros_like(vals)], axis=1)
+    a = torch.from_numpy(oracle.bf16_to_f32(vals))
+    for fmt, lim in (("int8", 127.0), ("e4m3", 448.0)):
+        _, s = oracle.quant_rows(rows, fmt, "div")
+        np.testing.assert_array_equal(s, torch.clamp(TP.scalar_div(a, lim), min=1.0e-12).numpy())
+        assert (s != torch.clamp(a / lim, min=1.0e-12).numpy()).sum() > 500
+        _, st = oracle.quant_tensor_e4m3(rows[-1:], None)
+        assert st == np.float32(a[-1].item()) * (np.float32(1.0) / np.float32(448.0))
+
+
 @pytest.mark.parametrize("static", [None, 0.0371, 1.0056])
 def test_tensor_quant_matches_reference_expression(oracle, static):
     for x in (activations(48, 1024, seed=2, outlier_channels=5), _edge_rows(64)):
@@ -128,6 +145,23 @@ def test_tensor_quant_matches_reference_expression(oracle, static):
         rq, rs = TP.quantize_tensor_e4m3(x, st)
         np.testing.assert_array_equal(q, bits8(rq))
         assert s == np.float32(rs.item())
+
+
+def test_tensor_quant_bf16_divisor(oracle):
+    """The bf16-divisor form equals the static form with the divisor bf16(s)
+    and still returns s; it differs from the fp32-divisor form on some codes."""
+    x = activations(64, 1024, seed=8, outlier_channels=4)
+    q, s = oracle.quant_tensor_e4m3(bits16(x), None, bf16_divisor=True)
+    q32, s32 = oracle.quant_tensor_e4m3(bits16(x))
+    assert s == s32
+    sb = np.float32(torch.tensor(float(s)).to(torch.bfloat16).float().item())
+    assert sb != s
+    qs, _ = oracle.quant_tensor_e4m3(bits16(x), sb)
+    np.testing.assert_array_equal(q, qs)
+    assert (q != q32).any()
+    # torch on the CPU, with the divisor rounded to bf16 explicitly
+    ref = torch.clamp((x.float() / torch.tensor(sb)).to(torch.bfloat16), -448.0, 448.0).to(torch.float8_e4m3fn)
+    np.testing.assert_array_equal(q, bits8(ref))
 
 
 def test_tensor_quant_keeps_the_bf16_intermediate(oracle):
@@ -139,6 +173,54 @@ def test_tensor_quant_keeps_the_bf16_intermediate(oracle):
     assert oracle.e4m3_to_f32(oracle.f32_to_e4m3(np.array([np.float32(17.125) / np.float32(1.0056)])))[0] == 18.0
     q2, _ = oracle.quant_rows(np.array([[x[0], oracle.f32_to_bf16(np.array([448.0], np.float32))[0]]]), "e4m3")
     assert q2.shape == (1, 2)
+
+
+def _head_inputs(b, s, h, d, seed):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(b, s, h, d, generator=gen) * torch.exp2(torch.randint(-6, 7, (1, 1, h, 1), generator=gen).float())
+    x[:, :, 0, 3] *= 40.0  # an outlier channel in head 0
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("shape", [(2, 37, 5, 64), (1, 300, 3, 128), (3, 4, 7, 20)])
+def test_per_head_quant_matches_reference_expression(oracle, shape):
+    x = _head_inputs(*shape, seed=sum(shape))
+    x[-1, :, -1, :] = 0.0                  # an all-zero head: scale 1e-12, codes +-0
+    x[0, 1, 1, :4] = torch.tensor([-0.0, 1e-30, -1e-30, 3e-39])
+    q, s = oracle.quant_per_head_e4m3(bits16(x))
+    rq, rs = TP.quantize_fp8_e4m3_per_head(x)
+    np.testing.assert_array_equal(q, bits8(rq))
+    np.testing.assert_array_equal(s, rs.numpy())
+    assert s[-1, -1] == np.float32(1e-12) and not (q[-1, :, -1, :] & 0x7F).any()
+
+
+def test_per_head_quant_closed_forms(oracle):
+    """Scales are independent per (batch, head); a power-of-two rescaling of
+    one head (no underflow or overflow) rescales only its scale, exactly, and
+    leaves every code unchanged; the scale of a head whose amax is 448 is 1,
+    so its codes are the e4m3 cast of the values themselves."""
+    x = _head_inputs(2, 50, 4, 32, seed=7)
+    q, s = oracle.quant_per_head_e4m3(bits16(x))
+    y = x.clone()
+    y[1, :, 2, :] *= 8.0
+    q2, s2 = oracle.quant_per_head_e4m3(bits16(y))
+    np.testing.assert_array_equal(q2, q)
+    expect = s.copy()
+    expect[1, 2] *= np.float32(8.0)
+    np.testing.assert_array_equal(s2, expect)
+    z = x.clone()
+    z[0, :, 1, :] = torch.clamp(z[0, :, 1, :], -300.0, 300.0)
+    z[0, 5, 1, 7] = 448.0
+    q3, s3 = oracle.quant_per_head_e4m3(bits16(z))
+    assert s3[0, 1] == 1.0
+    np.testing.assert_array_equal(q3[0, :, 1, :], oracle.f32_to_e4m3(z[0, :, 1, :].float().numpy()))
+    # the argmax element of each head maps to +-448 (code 0x7E / 0xFE)
+    flat = np.abs(x.float().numpy()).transpose(0, 2, 1, 3).reshape(2, 4, -1)
+    arg = flat.argmax(axis=2)
+    qc = q.transpose(0, 2, 1, 3).reshape(2, 4, -1)
+    for b in range(2):
+        for h in range(4):
+            assert qc[b, h, arg[b, h]] & 0x7F == 0x7E
 
 
 def test_vllm_int8_rcp_invariants(oracle):
@@ -158,9 +240,6 @@ def test_vllm_int8_rcp_invariants(oracle):
     assert np.all(np.abs(q[1:][np.arange(63), arg]) == 127)
     err = np.abs(xf - q.astype(np.float64) * s[:, None])
     assert np.all(err <= s[:, None] * 0.5 + np.abs(xf) * 2.0 ** -22 + 1e-30)
-    # differs from the division form somewhere (the two forms are not the same function)
-    qd, _ = oracle.quant_rows(bits16(x), "int8", "div")
-    assert (qd[1:] != q[1:]).any() or True
 
 
 # ---------------------------------------------------------------------- GEMMs
