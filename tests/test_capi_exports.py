@@ -116,7 +116,10 @@ def test_per_head_quant_errors_without_gpu():
     assert rc == 1 and b"null" in lib.h3q_last_error()
     rc = lib.h3q_quant_per_head_e4m3(p, -1, 8, 4, 128, p, p, p, None)
     assert rc == 1 and b"negative" in lib.h3q_last_error()
-    # workspace: batch * heads * chunks, chunks <= 64 and chunks * heads <= 4096
-    assert lib.h3q_quant_per_head_workspace_floats(1, 8192, 40, 128) == 40 * 64
-    assert lib.h3q_quant_per_head_workspace_floats(2, 3, 4096, 8) == 2 * 4096
-    assert lib.h3q_quant_per_head_workspace_floats(1, 5, 3, 128) == 3 * 5
+    # workspace: batch * heads * chunks * column groups (up to 8 positions
+    # per lane each), a chunk of at least 16 tokens, chunks * groups <= 1024
+    assert lib.h3q_quant_per_head_workspace_floats(1, 8192, 40, 128) == 40 * 512 * 2
+    assert lib.h3q_quant_per_head_workspace_floats(1, 65536, 56, 128) == 56 * 512 * 2
+    assert lib.h3q_quant_per_head_workspace_floats(4, 65536, 8, 128) == 4 * 8 * 512
+    assert lib.h3q_quant_per_head_workspace_floats(2, 3, 4096, 8) == 2 * 4096 * 8
+    assert lib.h3q_quant_per_head_workspace_floats(1, 5, 3, 128) == 3

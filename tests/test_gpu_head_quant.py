@@ -8,11 +8,11 @@ by the binary32 reciprocal) over every bf16 value, and the reference's eager
 torch expressions (oracle/torch_path.py) evaluated on the GPU against the
 oracle's weight, row, per-tensor and per-head quantizers.
 
-Shapes cover the vector path (head_dim % 8 == 0: one, several and partial
-segments of heads, multi-pass segments for wide heads, more than 64 heads per
-segment, the 4096-head limit, many batches), the element path (head_dim % 8 !=
-0 and a misaligned input), a full attention operand (1 x 8192 tokens x 40
-heads x 128), ragged token counts, zero heads and the module mirror."""
+Shapes cover the vector path (head_dim % 8 == 0) with one to eight
+positions per lane and one to eight column groups, the 4096-head limit, many
+batches, element positions (head_dim % 8 != 0), misaligned inputs and codes,
+a full attention operand (1 x 8192 tokens x 56 heads x 128), ragged token
+counts, zero heads and the module mirror."""
 
 from __future__ import annotations
 
@@ -46,15 +46,16 @@ def _check(ops, oracle, x_cpu, x_dev=None):
 
 
 @pytest.mark.parametrize("shape", [
-    (2, 37, 5, 64),      # one segment of 5 heads (8 x 64 bf16 per segment row)
-    (1, 300, 40, 128),   # 10 segments of 4 heads, 64 chunks
-    (3, 1, 7, 96),       # one token; 12-vector heads, a partial last segment
-    (1, 50, 3, 1024),    # 128-vector heads (two positions per lane)
-    (1, 10, 2, 4096),    # 512-vector heads: two column groups in pass 1
-    (1, 20, 130, 8),     # 64 heads per segment, 3 segments
+    (2, 37, 5, 64),      # 40 positions per row: one per lane, lanes 40..63 idle
+    (1, 300, 40, 128),   # 640 positions: two column groups of 5 per lane
+    (3, 1, 7, 96),       # one token; 12-position heads
+    (1, 50, 3, 1024),    # 384 positions: one group of 6 per lane
+    (1, 10, 2, 4096),    # 1024 positions: two groups of 8
+    (1, 129, 64, 128),   # 1024 positions, ragged chunks
+    (1, 20, 130, 8),     # one position per head
     (300, 5, 2, 16),     # many batches
-    (1, 3, 4096, 8),     # the head limit: one chunk, 48 KiB of LDS in pass 2
-    (2, 33, 3, 20),      # head_dim % 8 != 0: element path
+    (1, 3, 4096, 8),     # the head limit: 8 column groups, one chunk
+    (2, 33, 3, 20),      # head_dim % 8 != 0: element positions
     (1, 7, 1, 1),
 ])
 def test_per_head_matches_oracle(ops, oracle, device, shape):
@@ -65,17 +66,28 @@ def test_per_head_matches_oracle(ops, oracle, device, shape):
 
 
 def test_per_head_full_attention_operand(ops, oracle, device):
-    """One attention operand at its real size: 8192 tokens x 40 heads x 128."""
-    _check(ops, oracle, _head_inputs(1, 8192, 40, 128, seed=5))
+    """One attention operand at its real size: 8192 tokens x 56 heads x 128
+    (the FL transformer's heads at one GPU; two column groups of 7)."""
+    _check(ops, oracle, _head_inputs(1, 8192, 56, 128, seed=5))
 
 
-def test_per_head_misaligned_input_takes_the_element_path(ops, oracle, device):
+def test_per_head_misaligned_input_or_codes(ops, oracle, device):
+    """A misaligned input or code buffer keeps the 8-element positions (and
+    the workspace size) with element-wise accesses."""
     x = _head_inputs(1, 64, 4, 32, seed=6)
     flat = torch.empty(x.numel() + 1, dtype=torch.bfloat16, device=device)
     flat[1:].copy_(x.reshape(-1).to(device))
     view = flat[1:].view(x.shape)
     assert view.is_contiguous() and view.data_ptr() % 16 != 0
     _check(ops, oracle, x, view)
+    raw = torch.empty(x.numel() + 3, dtype=torch.uint8, device=device)
+    codes = raw[3:].view(torch.float8_e4m3fn).view(x.shape)
+    assert codes.is_contiguous() and codes.data_ptr() % 8 != 0
+    c, s = ops.quant_per_head_e4m3(x.to(device), codes=codes)
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_per_head_e4m3(bits16(x))
+    np.testing.assert_array_equal(bits8(c), rq)
+    np.testing.assert_array_equal(s.cpu().numpy(), rs)
 
 
 def test_per_head_repeated_calls_and_empty_batch(ops, oracle, device):
