@@ -13,10 +13,12 @@ FL/distributed/linear.py:16-181:
 * ``_module_fp8_input_scale`` and the two context managers keep FL's
   calibrated-scale protocol (FL/distributed/linear.py:16-47,104-128).
 
-This build runs on one GPU: tensor parallelism is represented (the same
-constructor arguments and weight-slicing helpers) but a ``ParallelContext``
-with more than one rank raises, since the collectives that TP needs are not
-part of it.
+This build runs on one GPU.  A ``ParallelContext`` may name any TP rank, so
+one rank's shard is sliced, loaded and run exactly as on a TP node (a
+column-parallel linear without output gather needs nothing from the other
+ranks); the steps that exchange data across ranks (the output gather of a
+column-parallel linear, the reduction of a row-parallel one) raise
+``NotImplementedError`` when the context has more than one rank.
 """
 
 from __future__ import annotations
@@ -35,14 +37,19 @@ from .. import ops
 
 @dataclass(frozen=True)
 class ParallelContext:
-    """Tensor-parallel placement of this rank (H3/distributed/parallel.py:9-31)."""
+    """Tensor-parallel placement of this rank (H3/distributed/parallel.py:9-31;
+    the process groups are not part of this single-GPU build)."""
 
     tp_world_size: int = 1
     tp_rank: int = 0
 
     def __post_init__(self) -> None:
-        if self.tp_world_size != 1 or self.tp_rank != 0:
-            raise NotImplementedError("tensor parallelism over several GPUs is not part of this single-GPU build")
+        if self.tp_world_size <= 0 or not 0 <= self.tp_rank < self.tp_world_size:
+            raise ValueError(f"invalid tp topology: world_size={self.tp_world_size}, rank={self.tp_rank}")
+
+
+def _cross_rank(what: str) -> NotImplementedError:
+    return NotImplementedError(f"{what} across tensor-parallel ranks is not part of this single-GPU build")
 
 
 _DEFAULT_CONTEXT = ParallelContext()
@@ -219,7 +226,10 @@ class ColumnParallelLinear(nn.Module):
         self.bias = nn.Parameter(torch.empty(self.local_output_size, dtype=dtype, device=device)) if bias else None
 
     def forward(self, inputs: torch.Tensor) -> torch.Tensor:
-        return _module_linear(self, inputs, self.bias)
+        output = _module_linear(self, inputs, self.bias)
+        if self.gather_output and self.tp_size > 1:
+            raise _cross_rank("gathering the output")
+        return output
 
     def full_weight_slice(self, value: torch.Tensor) -> torch.Tensor:
         if tuple(value.shape) != (self.output_size, self.input_size):
@@ -293,6 +303,8 @@ class RowParallelLinear(nn.Module):
         return _module_linear(self, inputs, None)
 
     def reduce_local_output(self, value: torch.Tensor) -> torch.Tensor:
+        if self.tp_size > 1:
+            raise _cross_rank("reducing the output")
         return value
 
     def forward(self, inputs: torch.Tensor) -> torch.Tensor:

@@ -25,6 +25,7 @@ quantizes straight into that layout, row chunk by row chunk.
 
 from __future__ import annotations
 
+from collections.abc import Callable
 from functools import lru_cache
 from typing import Any
 
@@ -133,21 +134,63 @@ def load_cutlass_w8a8_stream_weight_(module: Any, source_weight: torch.Tensor, *
         raise TypeError(f"{name} streamed CUTLASS W8A8 dtype differs")
     if source_weight.ndim != 2 or tuple(source_weight.shape) != tuple(module.weight.shape):
         raise ValueError(f"{name} streamed CUTLASS W8A8 shape differs")
+    stream_quantize_rows_(module, int(source_weight.shape[0]), int(source_weight.shape[1]),
+                          lambda start, stop: source_weight[start:stop], name=name,
+                          maximum_temporary_bytes=maximum_temporary_bytes)
+
+
+def stream_quantize_rows_(module: Any, rows: int, cols: int, fetch: Callable[[int, int], torch.Tensor], *,
+                          name: str, maximum_temporary_bytes: int = _STREAM_LOAD_TEMPORARY_BYTES) -> None:
+    """Fill a pending W8 slot from a bf16 [rows, cols] matrix that ``fetch(start,
+    stop)`` hands over in row ranges (a CPU or device tensor each; a streamed
+    checkpoint reads them from disk on demand).
+
+    Host rows go through two pinned staging buffers and two device buffers of
+    ``maximum_temporary_bytes / 2`` each, so the fetch of one chunk overlaps
+    the copy and quantization of the previous one, and the device staging
+    stays within the bound the reference sets (H3/inference/w8a8.py:105-133)."""
+    if getattr(module, "_cutlass_w8a8_stream_load_pending", None) is not True:
+        raise RuntimeError(f"{name} has no pending CUTLASS W8A8 stream load")
     if maximum_temporary_bytes <= 0:
         raise ValueError("maximum_temporary_bytes must be positive")
-    rows_per_chunk = max(1, maximum_temporary_bytes // (int(source_weight.shape[1]) * source_weight.element_size()))
     weight = module.weight
     scale = module._cutlass_w8a8_weight_scale
+    if weight.dtype != torch.int8 or tuple(weight.shape) != (rows, cols):
+        raise ValueError(f"{name} streamed CUTLASS W8A8 shape differs")
+    device = weight.device
     tiled = ops.is_tiled(weight)
-    for start in range(0, int(source_weight.shape[0]), rows_per_chunk):
-        stop = min(start + rows_per_chunk, int(source_weight.shape[0]))
-        temporary = source_weight[start:stop].to(device=weight.device, dtype=torch.bfloat16)
+    rows_per_chunk = max(1, min(rows, (maximum_temporary_bytes // 2) // (cols * 2)))
+    pinned: list[torch.Tensor | None] = [None, None]
+    staged = [torch.empty((rows_per_chunk, cols), dtype=torch.bfloat16, device=device) for _ in range(2)]
+    released: list[torch.cuda.Event | None] = [None, None]
+    stream = torch.cuda.current_stream(device)
+    for i, start in enumerate(range(0, rows, rows_per_chunk)):
+        stop = min(start + rows_per_chunk, rows)
+        n, b = stop - start, i % 2
+        chunk = fetch(start, stop)
+        if chunk.dtype != torch.bfloat16 or tuple(chunk.shape) != (n, cols):
+            raise ValueError(f"{name} streamed rows [{start}, {stop}) are not bf16 [{n}, {cols}]")
+        if chunk.device.type == "cpu":
+            if released[b] is not None:
+                released[b].synchronize()  # the copy that last read this pinned buffer is done
+            if pinned[b] is None:
+                pinned[b] = torch.empty((rows_per_chunk, cols), dtype=torch.bfloat16, pin_memory=True)
+            pinned[b][:n].copy_(chunk)
+            staged[b][:n].copy_(pinned[b][:n], non_blocking=True)
+            source = staged[b][:n]
+        else:
+            source = chunk.to(device=device)
         if tiled:
-            ops.quant_rows_tiled(temporary, ops.FMT_INT8, ops.ROUND_DIV, codes=weight.data, row0=start,
+            ops.quant_rows_tiled(source, ops.FMT_INT8, ops.ROUND_DIV, codes=weight.data, row0=start,
                                  scales=scale[start:stop])
         else:
-            ops.quant_rows(temporary, ops.FMT_INT8, ops.ROUND_DIV, codes=weight.data[start:stop],
+            ops.quant_rows(source, ops.FMT_INT8, ops.ROUND_DIV, codes=weight.data[start:stop],
                            scales=scale[start:stop])
+        released[b] = torch.cuda.Event()
+        released[b].record(stream)
+    for event in released:
+        if event is not None:
+            event.synchronize()
     module._cutlass_w8a8_stream_load_temporary_bytes_limit = int(maximum_temporary_bytes)
     module._cutlass_w8a8_stream_load_pending = False
     module._cutlass_w8a8_stream_loaded = True
@@ -331,4 +374,5 @@ __all__ = [
     "quantize_h3_interior_qkv_fc1_",
     "require_vllm_cutlass_w8a8",
     "resolve_h3_cutlass_w8a8_policy",
+    "stream_quantize_rows_",
 ]

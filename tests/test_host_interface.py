@@ -124,9 +124,32 @@ def test_bf16_module_linear_is_plain_linear():
     assert torch.allclose(m(x), torch.nn.functional.linear(x, m.weight, m.bias))
 
 
-def test_single_gpu_build_rejects_tensor_parallel_context():
-    with pytest.raises(NotImplementedError):
-        linear.ParallelContext(tp_world_size=2, tp_rank=0)
+def test_tensor_parallel_context_slices_locally_and_refuses_exchanges():
+    """A rank of a TP=2 context holds its shard; gathering or reducing across
+    ranks is outside the single-GPU build."""
+    with pytest.raises(ValueError):
+        linear.ParallelContext(tp_world_size=2, tp_rank=2)
+    ctx = linear.ParallelContext(tp_world_size=2, tp_rank=1)
+    col = linear.ColumnParallelLinear(4, 6, bias=True, gather_output=False, dtype=torch.float32, context=ctx)
+    full = torch.arange(24, dtype=torch.float32).reshape(6, 4)
+    assert torch.equal(col.full_weight_slice(full), full[3:])
+    assert torch.equal(col.full_bias_slice(torch.arange(6.0)), torch.arange(3.0, 6.0))
+    merged = linear.MergedColumnParallelLinear(4, [2, 4], bias=False, gather_output=False, dtype=torch.float32,
+                                               context=ctx)
+    assert torch.equal(merged.full_weight_slice(full), torch.cat([full[1:2], full[4:6]]))
+    row = linear.RowParallelLinear(4, 6, bias=False, dtype=torch.float32, context=ctx)
+    assert torch.equal(row.full_weight_slice(full), full[:, 2:])
+    with torch.no_grad():
+        col.weight.copy_(col.full_weight_slice(full))
+        col.bias.zero_()
+        row.weight.copy_(row.full_weight_slice(full))
+    x = torch.randn(2, 4)
+    assert torch.allclose(col(x), x @ full[3:].t())
+    gathered = linear.ColumnParallelLinear(4, 6, bias=False, gather_output=True, dtype=torch.float32, context=ctx)
+    with pytest.raises(NotImplementedError, match="across tensor-parallel ranks"):
+        gathered(x)
+    with pytest.raises(NotImplementedError, match="across tensor-parallel ranks"):
+        row(torch.randn(2, 2))
 
 
 def test_merged_column_weight_slice_keeps_logical_order():
