@@ -209,6 +209,40 @@ def bench_f1(torch, ops, dev) -> dict:
     return res
 
 
+def bench_a6(torch, ops, dev) -> dict:
+    """Row a6/a7: per-tensor e4m3fn activation quantization at the c2
+    activation shape (M=8192, K=5120), four rotating inputs.  Dynamic: two
+    launches (partial maxima, then fold + quantize), the input read twice;
+    static (a calibrated scale): one launch.  Algorithmic bytes: 2MK in + MK
+    out (+4)."""
+    gen = torch.Generator(device=dev).manual_seed(0)
+    m, k = M, K
+    xs = [gpu_randn(torch, (m, k), gen, dev) for _ in range(4)]
+    codes = torch.empty(m, k, device=dev, dtype=torch.float8_e4m3fn)
+    scale = torch.empty((), device=dev, dtype=torch.float32)
+    ws = torch.empty(int(ops._lib.lib().h3q_quant_tensor_workspace_floats(m, k)), device=dev, dtype=torch.float32)
+    static = torch.tensor(0.05, device=dev, dtype=torch.float32)
+
+    def dynamic(i):
+        ops.quant_tensor_e4m3(xs[i % 4], codes=codes, scale=scale, workspace=ws)
+
+    def calibrated(i):
+        ops.quant_tensor_e4m3(xs[i % 4], static, codes=codes, scale=scale)
+
+    for fn in (dynamic, calibrated):
+        for i in range(4):
+            fn(i)
+    torch.cuda.synchronize()
+    td = time_events(torch, dynamic, 40) * 1e3
+    ts = time_events(torch, calibrated, 40) * 1e3
+    byts = 3 * m * k + 4
+    del xs, codes
+    return {"M": m, "K": k, "dynamic_us": round(td, 1), "dynamic_GB/s": round(byts / td / 1e3, 1),
+            "dynamic_frac_hbm": round(byts / td / 1e3 / HBM_PEAK_GBS, 3), "static_us": round(ts, 1),
+            "static_GB/s": round(byts / ts / 1e3, 1), "static_frac_hbm": round(byts / ts / 1e3 / HBM_PEAK_GBS, 3),
+            "algorithmic_bytes": byts}
+
+
 def bench_f4(torch, ops, dev) -> dict:
     """Next row (f)4: per-(batch, head) FP8 quantization of one attention
     operand, [1, 8192, 56, 128] bf16 (the FL transformer's 56 heads of 128 at
@@ -451,7 +485,7 @@ def main() -> int:
     del xs, w, q_w, q_a, out
     torch.cuda.empty_cache()
     if not args.no_extra:
-        log("secondary configs: c3, c4, c5, f1, f4")
+        log("secondary configs: c3, c4, c5, f1, f4, a6")
         result["c3"] = bench_c3(torch, ops, dev)
         torch.cuda.empty_cache()
         result["c4"] = bench_c4(torch, ops, dev)
@@ -461,6 +495,8 @@ def main() -> int:
         result["f1"] = bench_f1(torch, ops, dev)
         torch.cuda.empty_cache()
         result["f4"] = bench_f4(torch, ops, dev)
+        torch.cuda.empty_cache()
+        result["a6"] = bench_a6(torch, ops, dev)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(torch, w_cpu, bias_cpu, x_cpu)

@@ -159,131 +159,209 @@ hipError_t launch_quant_rows_tiled(const uint16_t* x, int64_t ldx, int64_t rows,
 
 // ---------------------------------------------------------------- per-tensor
 
-// Pass 1: each workgroup reduces |x| over a contiguous band of rows.
-__global__ __launch_bounds__(256) void tensor_amax_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t rows,
-                                                          int64_t k, int64_t rows_per_block,
-                                                          float* __restrict__ partial) {
-    __shared__ float red[4];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
-    const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
-    const bool vec = (k % 8 == 0) && (ldx % 8 == 0) && ((uintptr_t)x % 16 == 0);
-    uint32_t m = 0;
-    float amax = 0.0f;
-    for (int64_t r = r0 + wave; r < r1; r += 4) {
-        const uint16_t* xr = x + r * ldx;
-        if (vec) {
-            const uint4* xv = reinterpret_cast<const uint4*>(xr);
-            for (int64_t j = lane; j < (k >> 3); j += 64) {
-                uint4 v = xv[j];
-                m = pk_abs_max(m, v.x);
-                m = pk_abs_max(m, v.y);
-                m = pk_abs_max(m, v.z);
-                m = pk_abs_max(m, v.w);
-            }
-        } else {
-            for (int64_t j = lane; j < k; j += 64) amax = fmaxf(amax, fabsf(bf16_lo(xr[j])));
-        }
-    }
-    amax = wave_max(fmaxf(amax, amax_from_packed(m)));
-    if (lane == 0) red[wave] = amax;
-    __syncthreads();
-    if (threadIdx.x == 0) partial[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
-
-// One element of the per-tensor quantizer: e4m3(clamp(bf16(x / s), +-448)).
+// One element of the per-tensor quantizer: e4m3(clamp(bf16(x / s), +-448)),
+// with x / s the correctly rounded binary32 quotient for any divisor.
 struct TensorQuant {
     float s, r;
-    bool exact_div;  // static scale or bf16 divisor: IEEE division
-    __device__ __forceinline__ float value(float f) const {
-        float qv = exact_div ? __fdiv_rn(f, s) : copysignf(div_rn(f, s, r), f);
-        return __builtin_amdgcn_fmed3f(round_to_bf16(qv), -kE4M3Max, kE4M3Max);
+    __device__ __forceinline__ float quotient(float f) const { return div_rn_any(f, s, r); }
+    // Two bf16 -> two codes: binary32 quotients, rounded to bf16 together
+    // (v_cvt_pk_bf16_f32, round to nearest even), clamped, converted.
+    __device__ __forceinline__ uint32_t pack2(uint32_t w) const {
+        const uint32_t b = pack_bf16x2(quotient(bf16_lo(w)), quotient(bf16_hi(w)));
+        return cvt_e4m3x2(__builtin_amdgcn_fmed3f(bf16_lo(b), -kE4M3Max, kE4M3Max),
+                          __builtin_amdgcn_fmed3f(bf16_hi(b), -kE4M3Max, kE4M3Max));
     }
-    __device__ __forceinline__ uint32_t pack4(uint32_t w0, uint32_t w1) const {
-        return cvt_e4m3x2(value(bf16_lo(w0)), value(bf16_hi(w0))) |
-               (cvt_e4m3x2(value(bf16_lo(w1)), value(bf16_hi(w1))) << 16);
-    }
+    __device__ __forceinline__ uint32_t pack4(uint32_t w0, uint32_t w1) const { return pack2(w0) | (pack2(w1) << 16); }
 };
 
-// Pass 2: every workgroup folds the partial maxima (or reads the static
-// scale), then quantizes its band of rows.
-// bf16_divisor: divide by bf16(s) (IEEE) instead of s, keeping s as the
-// returned scale.
-__global__ __launch_bounds__(256) void tensor_quant_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                           int64_t rows, int64_t k, int64_t rows_per_block,
-                                                           const float* __restrict__ partial, int nparts,
-                                                           const float* __restrict__ static_scale,
-                                                           int bf16_divisor, uint8_t* __restrict__ q,
-                                                           int64_t ldq, float* __restrict__ scale_out) {
-    __shared__ float red[4];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Maximum of a workgroup's per-wave values (non-negative), on every thread.
+__device__ __forceinline__ float block_max4(float v, float* red) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// Scale of pass 2: the static scale, or the fold of the partial maxima
+// (at most 1024: four loads per thread, issued together).
+__device__ __forceinline__ TensorQuant tensor_scale(const float* __restrict__ partial, int nparts,
+                                                    const float* __restrict__ static_scale, int bf16_divisor,
+                                                    float* red, float* __restrict__ scale_out) {
     TensorQuant tq;
     if (static_scale) {
         tq.s = *static_scale;
-        tq.exact_div = true;
     } else {
-        float a = 0.0f;
-        for (int i = threadIdx.x; i < nparts; i += 256) a = fmaxf(a, partial[i]);
-        a = wave_max(a);
-        if (lane == 0) red[wave] = a;
-        __syncthreads();
-        a = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        float p[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = (int)threadIdx.x + 256 * k;
+            p[k] = partial[i < nparts ? i : nparts - 1];
+        }
+        const float a = block_max4(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])), red);
         tq.s = amax_scale(a, kE4M3Recip);
-        tq.exact_div = false;
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = tq.s;
-    if (bf16_divisor) {
-        tq.s = round_to_bf16(tq.s);
-        tq.exact_div = true;
-    }
+    if (bf16_divisor) tq.s = round_to_bf16(tq.s);
     tq.r = 1.0f / tq.s;
-    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
-    const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
-    const bool vec = (k % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && ((uintptr_t)x % 16 == 0) &&
-                     ((uintptr_t)q % 8 == 0);
-    for (int64_t r = r0 + wave; r < r1; r += 4) {
-        const uint16_t* xr = x + r * ldx;
-        uint8_t* qr = q + r * ldq;
-        if (vec) {
-            const uint4* xv = reinterpret_cast<const uint4*>(xr);
-            uint2* qv = reinterpret_cast<uint2*>(qr);
-            for (int64_t j = lane; j < (k >> 3); j += 64) {
-                uint4 v = xv[j];
+    return tq;
+}
+
+// Vector path (K % 8 == 0, 16-byte aligned rows, K <= NV * 512): one wave per
+// row, NV 16-byte loads per lane issued together.  Lanes past the row re-read
+// its last vector (harmless for a maximum; their codes are not stored).
+template <int NV>
+__global__ __launch_bounds__(256) void tensor_amax_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                              int64_t rows, int k, float* __restrict__ partial) {
+    __shared__ float red[4];
+    const int lane = threadIdx.x & 63;
+    const int nvec = k >> 3;
+    int off[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) off[i] = (i * 64 + lane < nvec ? i * 64 + lane : nvec - 1) * 8;
+    uint32_t m = 0;
+    const int64_t step = (int64_t)gridDim.x * 4;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += step) {
+        const uint16_t* xr = x + row * ldx;
+        uint4 v[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) v[i] = *reinterpret_cast<const uint4*>(xr + off[i]);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            m = pk_abs_max(m, v[i].x);
+            m = pk_abs_max(m, v[i].y);
+            m = pk_abs_max(m, v[i].z);
+            m = pk_abs_max(m, v[i].w);
+        }
+    }
+    const float a = block_max4(amax_from_packed(m), red);
+    if (threadIdx.x == 0) partial[blockIdx.x] = a;
+}
+
+// bf16_divisor: divide by bf16(s) (IEEE) instead of s, keeping s as the
+// returned scale.
+template <int NV>
+__global__ __launch_bounds__(256) void tensor_quant_vec_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                               int64_t rows, int k, const float* __restrict__ partial,
+                                                               int nparts, const float* __restrict__ static_scale,
+                                                               int bf16_divisor, uint8_t* __restrict__ q,
+                                                               int64_t ldq, float* __restrict__ scale_out) {
+    __shared__ float red[4];
+    const TensorQuant tq = tensor_scale(partial, nparts, static_scale, bf16_divisor, red, scale_out);
+    const int lane = threadIdx.x & 63;
+    const int nvec = k >> 3;
+    int off[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) off[i] = (i * 64 + lane < nvec ? i * 64 + lane : nvec - 1) * 8;
+    const int64_t step = (int64_t)gridDim.x * 4;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < rows; row += step) {
+        const uint16_t* xr = x + row * ldx;
+        uint8_t* qr = q + row * ldq;
+        uint4 v[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) v[i] = *reinterpret_cast<const uint4*>(xr + off[i]);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            if (i * 64 + lane < nvec) {
                 uint2 o;
-                o.x = tq.pack4(v.x, v.y);
-                o.y = tq.pack4(v.z, v.w);
-                qv[j] = o;
+                o.x = tq.pack4(v[i].x, v[i].y);
+                o.y = tq.pack4(v[i].z, v[i].w);
+                *reinterpret_cast<uint2*>(qr + off[i]) = o;
             }
-        } else {
-            for (int64_t j = lane; j < k; j += 64) qr[j] = (uint8_t)(tq.pack4(xr[j], 0u) & 0xFFu);
         }
     }
 }
 
+// General path (any K and alignment): elementwise, a band of rows per workgroup.
+__global__ __launch_bounds__(256) void tensor_amax_any_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                              int64_t rows, int64_t k, int64_t rows_per_block,
+                                                              float* __restrict__ partial) {
+    __shared__ float red[4];
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+    const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
+    float amax = 0.0f;
+    for (int64_t r = r0; r < r1; ++r)
+        for (int64_t j = threadIdx.x; j < k; j += 256) amax = fmaxf(amax, fabsf(bf16_lo(x[r * ldx + j])));
+    const float a = block_max4(amax, red);
+    if (threadIdx.x == 0) partial[blockIdx.x] = a;
+}
+
+__global__ __launch_bounds__(256) void tensor_quant_any_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                               int64_t rows, int64_t k, int64_t rows_per_block,
+                                                               const float* __restrict__ partial, int nparts,
+                                                               const float* __restrict__ static_scale,
+                                                               int bf16_divisor, uint8_t* __restrict__ q,
+                                                               int64_t ldq, float* __restrict__ scale_out) {
+    __shared__ float red[4];
+    const TensorQuant tq = tensor_scale(partial, nparts, static_scale, bf16_divisor, red, scale_out);
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+    const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
+    for (int64_t r = r0; r < r1; ++r)
+        for (int64_t j = threadIdx.x; j < k; j += 256) q[r * ldq + j] = (uint8_t)(tq.pack2(x[r * ldx + j]) & 0xFFu);
+}
+
+namespace {
+
+constexpr int64_t kTensorBlocks = 1024;
+
+int64_t tensor_blocks(int64_t rows) { return (rows + 3) / 4 < kTensorBlocks ? (rows + 3) / 4 : kTensorBlocks; }
+
+bool tensor_vec(const uint16_t* x, int64_t ldx, int64_t k, const uint8_t* q, int64_t ldq) {
+    return k % 8 == 0 && ldx % 8 == 0 && ldq % 8 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)q % 8 == 0 &&
+           (k + 511) / 512 <= 32;
+}
+
+template <int NV>
+hipError_t launch_tensor_vec(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k, const float* static_scale,
+                             bool bf16_divisor, float* partial, uint8_t* q, int64_t ldq, float* scale_out,
+                             hipStream_t st) {
+    const int64_t blocks = tensor_blocks(rows);
+    if (!static_scale) {
+        hipLaunchKernelGGL((tensor_amax_vec_kernel<NV>), dim3((unsigned)blocks), dim3(256), 0, st, x, ldx, rows,
+                           (int)k, partial);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((tensor_quant_vec_kernel<NV>), dim3((unsigned)blocks), dim3(256), 0, st, x, ldx, rows, (int)k,
+                       (const float*)partial, (int)blocks, static_scale, (int)bf16_divisor, q, ldq, scale_out);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// Partial maxima written by pass 1: one per workgroup of either path.
 int64_t tensor_quant_parts(int64_t rows, int64_t k) {
-    // Enough bands to fill the chip for the amax pass, few enough that every
-    // workgroup of the second pass folds them quickly.
-    const int64_t elems = rows * k;
-    int64_t parts = (elems + 65535) / 65536;
-    if (parts > 1024) parts = 1024;
-    if (parts > rows) parts = rows;
-    return parts < 1 ? 1 : parts;
+    (void)k;
+    return rows < 1 ? 1 : (rows < kTensorBlocks ? rows : kTensorBlocks);
 }
 
 hipError_t launch_quant_tensor_e4m3(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k,
                                     const float* static_scale, bool bf16_divisor, float* partial, uint8_t* q,
                                     int64_t ldq, float* scale_out, hipStream_t st) {
-    const int64_t parts = tensor_quant_parts(rows, k);
-    const int64_t rpb = (rows + parts - 1) / parts;
-    const int64_t blocks = (rows + rpb - 1) / rpb;
+    if (tensor_vec(x, ldx, k, q, ldq)) {
+        const int64_t nv = (k + 511) / 512;
+        if (nv <= 2) return launch_tensor_vec<2>(x, ldx, rows, k, static_scale, bf16_divisor, partial, q, ldq, scale_out, st);
+        if (nv <= 4) return launch_tensor_vec<4>(x, ldx, rows, k, static_scale, bf16_divisor, partial, q, ldq, scale_out, st);
+        if (nv <= 8) return launch_tensor_vec<8>(x, ldx, rows, k, static_scale, bf16_divisor, partial, q, ldq, scale_out, st);
+        if (nv <= 10) return launch_tensor_vec<10>(x, ldx, rows, k, static_scale, bf16_divisor, partial, q, ldq, scale_out, st);
+        if (nv <= 11) return launch_tensor_vec<11>(x, ldx, rows, k, static_scale, bf16_divisor, partial, q, ldq, scale_out, st);
+        if (nv <= 14) return launch_tensor_vec<14>(x, ldx, rows, k, static_scale, bf16_divisor, partial, q, ldq, scale_out, st);
+        if (nv <= 16) return launch_tensor_vec<16>(x, ldx, rows, k, static_scale, bf16_divisor, partial, q, ldq, scale_out, st);
+        if (nv <= 24) return launch_tensor_vec<24>(x, ldx, rows, k, static_scale, bf16_divisor, partial, q, ldq, scale_out, st);
+        if (nv <= 28) return launch_tensor_vec<28>(x, ldx, rows, k, static_scale, bf16_divisor, partial, q, ldq, scale_out, st);
+        return launch_tensor_vec<32>(x, ldx, rows, k, static_scale, bf16_divisor, partial, q, ldq, scale_out, st);
+    }
+    // Bands of rows: at most 1024 workgroups (the fold reads one partial each).
+    const int64_t blocks = rows < kTensorBlocks ? rows : kTensorBlocks;
+    const int64_t rpb = (rows + blocks - 1) / blocks;
+    const int64_t used = (rows + rpb - 1) / rpb;
     if (!static_scale) {
-        hipLaunchKernelGGL(tensor_amax_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, ldx, rows, k, rpb,
+        hipLaunchKernelGGL(tensor_amax_any_kernel, dim3((unsigned)used), dim3(256), 0, st, x, ldx, rows, k, rpb,
                            partial);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(tensor_quant_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, ldx, rows, k, rpb,
-                       (const float*)partial, (int)blocks, static_scale, (int)bf16_divisor, q, ldq, scale_out);
+    hipLaunchKernelGGL(tensor_quant_any_kernel, dim3((unsigned)used), dim3(256), 0, st, x, ldx, rows, k, rpb,
+                       (const float*)partial, (int)used, static_scale, (int)bf16_divisor, q, ldq, scale_out);
     return hipGetLastError();
 }
 

@@ -38,6 +38,22 @@ H3Q_HD float div_rn(float x, float s, float r) {
     return fmaf(e, r, q0);
 }
 
+// The same quotient for any binary32 divisor (a static, calibrated scale or
+// one rounded to bf16): where the three operations leave a non-finite value
+// (the quotient or the reciprocal overflows, s is 0, inf or NaN, x is inf or
+// NaN), the IEEE division decides.  The test suite checks that the finite
+// results, rounded to bf16 as the per-tensor quantizer rounds them, equal
+// those of IEEE division over every bf16 numerator and every bf16 divisor,
+// and over a sweep of binary32 divisors.
+// (For x = +-0 the correction loses the sign of the zero quotient; the first
+// product has it.)
+H3Q_HD float div_rn_any(float x, float s, float r) {
+    const float q0 = x * r;
+    const float q1 = fmaf(fmaf(-q0, s, x), r, q0);
+    if (isfinite(q1)) return x == 0.0f ? q0 : q1;
+    return x / s;
+}
+
 // Scale of a dynamic quantizer from its absolute maximum:
 //   s = max(RN(amax * RN(1/limit)), 1e-12)
 // The reference writes torch.clamp(amax.float() / limit, min=1.0e-12)
