@@ -22,7 +22,7 @@ NAMES = [f"blocks.{b}.{p}" for b in range(50) for p in ("attn.qkv_proj", "attn.o
 def test_int8_policy_selects_interior_qkv_and_fc1():
     sel = w8a8.resolve_h3_cutlass_w8a8_policy(NAMES, policy="interior_fc1_qkv_v1")
     q = sel["quantized_linear_names"]
-    assert len(q) == 90  # blocks 2..46, qkv + fc1 (SURVEY: 90 linears)
+    assert len(q) == 90  # blocks 2..46, qkv + fc1: 90 linears
     assert all(n.endswith((".attn.qkv_proj", ".mlp.fc1")) for n in q)
     assert {int(n.split(".")[1]) for n in q} == set(range(2, 47))
     assert sel["bf16_boundary_block_indices"] == [0, 1, 47, 48, 49]
