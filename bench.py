@@ -174,7 +174,8 @@ def bench_f1(torch, ops, dev) -> dict:
     steps unfused (modulated bf16 rows written, then re-read by the
     quantizer).  At the c2 activation shape and at the real H3 QKV input
     (1088x1920 phase 0, M=6224, K=5376); four rotating inputs, four table rows.
-    Bytes: fused 2MK in + MK + 4M out; unfused adds 4MK."""
+    Bytes: fused 2MK in + MK + 4M out; unfused adds 4MK.  Then the fc2-input
+    producer (SwiGLU + e4m3 act-quant) the same way."""
     res = {}
     for name, m, k in (("c2_shape", 8192, 5120), ("h3_qkv_1088p", 6224, 5376)):
         gen = torch.Generator(device=dev).manual_seed(0)
@@ -206,6 +207,34 @@ def bench_f1(torch, ops, dev) -> dict:
                      "fused_GB/s": round(byts / tf / 1e3, 1), "frac_hbm": round(byts / tf / 1e3 / HBM_PEAK_GBS, 3),
                      "saved_bytes": 4 * m * k}
         del xs, codes, y
+    # The fc2-input producer: SwiGLU of [M, 2F] with the per-token e4m3
+    # quantizer folded in, at c3's FFN width (F = 13824).  Bytes: fused 4MF in
+    # + MF + 4M out; unfused adds 4MF (bf16 rows written, then re-read).
+    m, f = 8192, 13824
+    gen = torch.Generator(device=dev).manual_seed(0)
+    xs = [gpu_randn(torch, (m, 2 * f), gen, dev, 2.0) for _ in range(4)]
+    codes = torch.empty(m, f, device=dev, dtype=torch.float8_e4m3fn)
+    scales = torch.empty(m, 1, device=dev, dtype=torch.float32)
+    y = torch.empty(m, f, device=dev, dtype=torch.bfloat16)
+
+    def sw_fused(i):
+        ops.swiglu_quant(xs[i % 4], fmt=ops.FMT_E4M3FN, codes=codes, scales=scales)
+
+    def sw_unfused(i):
+        ops.swiglu_quant(xs[i % 4], out=y)
+        ops.quant_rows(y, ops.FMT_E4M3FN, ops.ROUND_DIV, codes=codes, scales=scales)
+
+    for fn in (sw_fused, sw_unfused):
+        for i in range(4):
+            fn(i)
+    torch.cuda.synchronize()
+    tf = time_events(torch, sw_fused, 20) * 1e3
+    tu = time_events(torch, sw_unfused, 20) * 1e3
+    byts = 5 * m * f + 4 * m
+    res["swiglu_c3_width"] = {"M": m, "F": f, "fused_us": round(tf, 1), "unfused_us": round(tu, 1),
+                              "fused_GB/s": round(byts / tf / 1e3, 1),
+                              "frac_hbm": round(byts / tf / 1e3 / HBM_PEAK_GBS, 3), "saved_bytes": 4 * m * f}
+    del xs, codes, y
     return res
 
 

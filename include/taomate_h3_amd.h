@@ -128,6 +128,22 @@ int h3q_quant_tensor_e4m3_bf16_divisor(const void* x, int64_t rows, int64_t cols
                                        float* scale_out, void* stream);
 
 /*
+ * Fused SwiGLU, optionally with the per-token quantization of the result:
+ *   x: bf16 [rows, 2 * half] (leading dimension ldx), each row [gate | up]
+ *   y = bf16(bf16(gate / (1 + exp(-gate))) * up)           bf16 [rows, half]
+ * to out (leading dimension ldo; NULL for none) and / or codes [rows, half]
+ * (ldq bytes) + fp32 scales [rows] in the format / rounding of
+ * h3q_quant_rows.  Replaces fused_swiglu (H3/inference/fused_kernels.py:240-261,
+ * 663-677) and the eager F.silu(gate) * up (H3/model/layers.py:469-479) that
+ * produce the fc2 input, with the next W8A8 linear's act-quant folded in.  exp
+ * is computed from IEEE multiply-adds (within 1 ulp of a correctly rounded
+ * exp); the division and product are IEEE.  half % 8 == 0, half <= 16384,
+ * 16-byte aligned x / out, strides multiples of 8 elements.
+ */
+int h3q_swiglu_quant(const void* x, int64_t ldx, int64_t rows, int64_t half, void* out, int64_t ldo, int format,
+                     int rounding, void* codes, int64_t ldq, float* scales, void* stream);
+
+/*
  * Per-(batch, head) e4m3fn quantization of attention operands:
  *   x: contiguous bf16 [batch, seq, heads, head_dim]
  *   scales[b, h] = max(amax_{s,d}(|x[b, s, h, d]|) * RN(1/448), 1e-12)   (fp32 [batch, heads])

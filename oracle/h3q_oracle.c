@@ -17,6 +17,10 @@
  *   orc_quant_tensor_e4m3      FL/inference/fused_kernels.py:771-796 (eager) and
  *                              :140-172,230-247 (Triton: bf16 intermediate);
  *                              FL/inference/fp8.py:259-263 (weights)
+ *   orc_exp_f32, orc_swiglu    the fused SwiGLU producer's arithmetic: torch's silu
+ *                              x / (1 + exp(-x)) rounded to bf16, times up, rounded
+ *                              (H3/model/layers.py:469-479; H3/inference/fused_kernels.py:
+ *                              240-261), with the kernel's own exp restated
  *   orc_quant_per_head_e4m3    FL/inference/fused_kernels.py:823-877 (eager :826-834;
  *                              Triton :175-227, :250-273): per-(batch, head) scale,
  *                              fp32 quotient
@@ -206,6 +210,44 @@ ORC_API void orc_quant_per_head_e4m3(const uint16_t* x, int64_t batch, int64_t s
                     q[off + d] = orc_f32_to_e4m3(v);
                 }
             }
+        }
+    }
+}
+
+/* exp(x) as the fused SwiGLU kernel computes it: x = k ln2 + r, k = rint(x / ln2),
+ * r reduced with a two-term ln2 (Cody and Waite), degree-7 Taylor polynomial of
+ * e^r in Horner form with fused multiply-adds, then ldexp by k.  The constants
+ * are binary32 roundings of ln 2, 1/ln 2 and 1/n!.  Pinned against the C
+ * library's expf (within 1 ulp). */
+ORC_API float orc_exp_f32(float x) {
+    if (x > 0x1.62e430p+6f) return INFINITY;
+    if (x < -0x1.9fe368p+6f) return 0.0f;
+    const float k = rintf(x * 0x1.715476p+0f);
+    float r = fmaf(-k, 0x1.62e430p-1f, x);
+    r = fmaf(-k, -0x1.05c610p-29f, r);
+    float p = 0x1.a01a02p-13f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0x1.0p-1f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)k);
+}
+
+/* SwiGLU of rows [gate (half) | up (half)] (bf16 bits, leading dimension ldx):
+ *   s = bf16(gate / (1 + exp(-gate)));  y = bf16(s * up)
+ * torch's silu on a bf16 tensor computes x / (1 + exp(-x)) in binary32 and
+ * rounds to bf16; the product of two bf16 is exact in binary32 and rounded
+ * once (H3/model/layers.py:478: F.silu(gate) * up). */
+ORC_API void orc_swiglu(const uint16_t* x, int64_t rows, int64_t half, int64_t ldx, uint16_t* y, int64_t ldy) {
+    for (int64_t i = 0; i < rows; ++i) {
+        for (int64_t j = 0; j < half; ++j) {
+            const float g = orc_bf16_to_f32(x[i * ldx + j]);
+            const float u = orc_bf16_to_f32(x[i * ldx + half + j]);
+            const float s = orc_bf16_to_f32(orc_f32_to_bf16(g / (1.0f + orc_exp_f32(-g))));
+            y[i * ldy + j] = orc_f32_to_bf16(s * u);
         }
     }
 }

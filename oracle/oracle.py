@@ -67,6 +67,10 @@ def _load() -> ctypes.CDLL:
         fn.argtypes = [_p, _i64, _i64, _i64, _p, _i64, _p]
     lib.orc_quant_tensor_e4m3.restype = None
     lib.orc_quant_tensor_e4m3.argtypes = [_p, _i64, _i64, _i64, _p, ctypes.c_int, _p, _i64, _p]
+    lib.orc_exp_f32.restype = ctypes.c_float
+    lib.orc_exp_f32.argtypes = [ctypes.c_float]
+    lib.orc_swiglu.restype = None
+    lib.orc_swiglu.argtypes = [_p, _i64, _i64, _i64, _p, _i64]
     lib.orc_quant_per_head_e4m3.restype = None
     lib.orc_quant_per_head_e4m3.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _p]
     lib.orc_gemm_i8_i32.restype = None
@@ -178,6 +182,24 @@ def quant_tensor_e4m3(x_bits: np.ndarray, static_scale: float | None = None,
     st = None if static_scale is None else np.array([static_scale], dtype=np.float32)
     lib.orc_quant_tensor_e4m3(_ptr(x), rows, k, k, _ptr(st), int(bf16_divisor), _ptr(codes), k, _ptr(scale))
     return codes.reshape(np.shape(x_bits)), scale[0]
+
+
+def exp_f32(x: np.ndarray) -> np.ndarray:
+    """The fused SwiGLU kernel's binary32 exp, elementwise."""
+    lib = _load()
+    flat = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    return np.array([lib.orc_exp_f32(float(v)) for v in flat], dtype=np.float32).reshape(np.shape(x))
+
+
+def swiglu(x_bits: np.ndarray) -> np.ndarray:
+    """bf16 bits [rows, 2 * half] ([gate | up]) -> y bits [rows, half]."""
+    lib = _load()
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    rows, width = x.shape
+    half = width // 2
+    y = np.empty((rows, half), dtype=np.uint16)
+    lib.orc_swiglu(_ptr(x), rows, half, width, _ptr(y), half)
+    return y
 
 
 def quant_per_head_e4m3(x_bits: np.ndarray) -> tuple[np.ndarray, np.ndarray]:

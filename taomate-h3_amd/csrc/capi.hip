@@ -221,6 +221,44 @@ __attribute__((visibility("default"))) int h3q_quant_tensor_e4m3_bf16_divisor(co
                              codes, ldq, scale_out, stream);
 }
 
+__attribute__((visibility("default"))) int h3q_swiglu_quant(const void* x, int64_t ldx, int64_t rows, int64_t half,
+                                                            void* out, int64_t ldo, int format, int rounding,
+                                                            void* codes, int64_t ldq, float* scales, void* stream) {
+    const char* who = "h3q_swiglu_quant";
+    if (rows < 0 || half <= 0) return fail(H3Q_ERR_INVALID, "%s: bad shape [%lld, 2 x %lld]", who, (long long)rows, (long long)half);
+    if (half % 8) return fail(H3Q_ERR_UNSUPPORTED, "%s: half=%lld must be a multiple of 8", who, (long long)half);
+    if (half > h3q::kSwigluMaxHalf)
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: half=%lld above %d", who, (long long)half, h3q::kSwigluMaxHalf);
+    if (ldx < 2 * half || ldx % 8) return fail(H3Q_ERR_INVALID, "%s: bad input stride %lld", who, (long long)ldx);
+    if (!out && !codes) return fail(H3Q_ERR_INVALID, "%s: neither a bf16 output nor codes requested", who);
+    if (out && (ldo < half || ldo % 8 || !aligned(out, 16)))
+        return fail(H3Q_ERR_INVALID, "%s: output needs a stride >= half, a multiple of 8, and 16-byte alignment", who);
+    if (codes) {
+        if (format != H3Q_FMT_E4M3FN && format != H3Q_FMT_INT8)
+            return fail(H3Q_ERR_INVALID, "%s: unknown format %d", who, format);
+        if (rounding != H3Q_ROUND_DIV && rounding != H3Q_ROUND_RCP_MUL)
+            return fail(H3Q_ERR_INVALID, "%s: unknown rounding %d", who, rounding);
+        if (format == H3Q_FMT_E4M3FN && rounding != H3Q_ROUND_DIV)
+            return fail(H3Q_ERR_UNSUPPORTED, "%s: e4m3fn codes use the division form only", who);
+        if (ldq < half || ldq % 8 || !aligned(codes, 8))
+            return fail(H3Q_ERR_INVALID, "%s: codes need a stride >= half, a multiple of 8, and 8-byte alignment", who);
+        if (!scales) return fail(H3Q_ERR_INVALID, "%s: codes need a scales pointer", who);
+    }
+    if (rows == 0) return ok();
+    if (!x || !aligned(x, 16)) return fail(H3Q_ERR_INVALID, "%s: x must be non-null and 16-byte aligned", who);
+    h3q::SwigluQuantArgs a{};
+    a.x = (const uint16_t*)x;
+    a.ldx = ldx;
+    a.rows = rows;
+    a.half = (int)half;
+    a.out = (uint16_t*)out;
+    a.ldo = ldo;
+    a.codes = (uint8_t*)codes;
+    a.ldq = ldq;
+    a.scales = scales;
+    return check_launch(h3q::launch_swiglu_quant(a, format, rounding, (hipStream_t)stream), who);
+}
+
 __attribute__((visibility("default"))) int64_t h3q_quant_per_head_workspace_floats(int64_t batch, int64_t seq,
                                                                                    int64_t heads, int64_t head_dim) {
     if (batch <= 0 || seq <= 0 || heads <= 0 || head_dim <= 0 || heads > h3q::kMaxHeads) return 1;

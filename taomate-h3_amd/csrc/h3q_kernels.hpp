@@ -21,6 +21,23 @@ hipError_t launch_quant_tensor_e4m3(const uint16_t* x, int64_t ldx, int64_t rows
                                     const float* static_scale, bool bf16_divisor, float* partial, uint8_t* q,
                                     int64_t ldq, float* scale_out, hipStream_t st);
 
+// Fused SwiGLU (+ per-token quantization): rows of x are [gate (half) | up
+// (half)] bf16; y = bf16(bf16(silu(gate)) * up) to out (optional, [rows, half])
+// and / or its codes + scales.  half % 8 == 0, half <= kSwigluMaxHalf, 16-byte
+// aligned rows.
+struct SwigluQuantArgs {
+    const uint16_t* x;
+    int64_t ldx, rows;
+    int half;
+    uint16_t* out;
+    int64_t ldo;
+    uint8_t* codes;
+    int64_t ldq;
+    float* scales;
+};
+constexpr int kSwigluMaxHalf = 16384;
+hipError_t launch_swiglu_quant(const SwigluQuantArgs& a, int fmt, int rounding, hipStream_t st);
+
 // Per-(batch, head) e4m3fn quantization of a contiguous [batch, seq, heads,
 // head_dim] bf16 tensor: codes of the same shape, scales [batch, heads].
 // partial holds per_head_quant_parts(...) floats.

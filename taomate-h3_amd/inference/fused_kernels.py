@@ -106,6 +106,36 @@ def quantize_fp8_e4m3_rowwise(value: torch.Tensor) -> tuple[torch.Tensor, torch.
     return codes.reshape(shape), scales.reshape(*shape[:-1], 1)
 
 
+def fused_swiglu(value: torch.Tensor) -> torch.Tensor:
+    """SwiGLU of ``value [..., 2F]`` ([gate | up]) -> ``[..., F]`` bf16
+    (H3/inference/fused_kernels.py:663-677; the eager F.silu(gate) * up of
+    H3/model/layers.py:476-479): bf16(bf16(gate / (1 + exp(-gate))) * up)."""
+    _as_bf16(value, "fused_swiglu")
+    shape = value.shape
+    flat = value.reshape(-1, int(shape[-1]))
+    if flat.stride(-1) != 1 or flat.data_ptr() % 16 or (flat.shape[0] > 1 and flat.stride(0) % 8):
+        flat = flat.contiguous()
+    out, _, _ = ops.swiglu_quant(flat, out=True)
+    return out.reshape(*shape[:-1], int(shape[-1]) // 2)
+
+
+def fused_swiglu_w8a8(value: torch.Tensor, *, fmt: int = ops.FMT_INT8,
+                      keep_dense: bool = False) -> QuantizedActivations:
+    """``fused_swiglu`` with the per-token quantizer of the fc2 W8A8 linear
+    folded in (int8 in vLLM's form, or e4m3fn): the fc2 input is never
+    written and re-read in bf16 (unless ``keep_dense``)."""
+    _as_bf16(value, "fused_swiglu_w8a8")
+    shape = value.shape
+    flat = value.reshape(-1, int(shape[-1]))
+    if flat.stride(-1) != 1 or flat.data_ptr() % 16 or (flat.shape[0] > 1 and flat.stride(0) % 8):
+        flat = flat.contiguous()
+    rounding = ops.ROUND_RCP_MUL if fmt == ops.FMT_INT8 else ops.ROUND_DIV
+    dense, codes, scales = ops.swiglu_quant(flat, fmt=fmt, rounding=rounding, out=keep_dense)
+    out_shape = (*shape[:-1], int(shape[-1]) // 2)
+    return QuantizedActivations(codes, scales, out_shape, fmt,
+                                None if dense is None else dense.reshape(out_shape))
+
+
 @dataclass
 class QuantizedActivations:
     """Per-token codes of a linear's input: ``codes [M, K]`` (row-major),
@@ -202,7 +232,8 @@ def fused_residual_gate_rms_norm_modulate_w8a8(residual: torch.Tensor, branch: t
 
 
 __all__ = ["FP8_MAX", "QuantizedActivations", "as_dense", "enable_h3_inference_fused_kernels",
-           "enable_h3_sol_engine_fusions", "fused_residual_gate_rms_norm_modulate", "h3_inference_fused_kernels_enabled",
+           "enable_h3_sol_engine_fusions", "fused_residual_gate_rms_norm_modulate", "fused_swiglu",
+           "fused_swiglu_w8a8", "h3_inference_fused_kernels_enabled",
            "fused_residual_gate_rms_norm_modulate_w8a8", "fused_rms_norm_modulate", "fused_rms_norm_modulate_w8a8",
            "quantize_fp8_e4m3", "quantize_fp8_e4m3_dynamic", "quantize_fp8_e4m3_per_head",
            "quantize_fp8_e4m3_rowwise"]

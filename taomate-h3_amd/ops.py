@@ -269,6 +269,48 @@ def quant_tensor_e4m3(x: torch.Tensor, static_scale: torch.Tensor | None = None,
     return codes, scale
 
 
+def swiglu_quant(x: torch.Tensor, *, fmt: int | None = None, rounding: int = ROUND_DIV,
+                 out: torch.Tensor | bool | None = None, codes: torch.Tensor | None = None,
+                 scales: torch.Tensor | None = None):
+    """Fused SwiGLU of bf16 rows ``x [rows, 2 * half]`` ([gate | up]):
+    y = bf16(bf16(gate / (1 + exp(-gate))) * up), to ``out`` (a bf16 tensor,
+    True to allocate one, None/False for none) and / or per-token codes in
+    ``fmt`` (None: no codes).  Returns (out or None, codes or None, scales or None)."""
+    want_out = out is True or isinstance(out, torch.Tensor)
+    _require_gpu("swiglu_quant", x, out if isinstance(out, torch.Tensor) else None, codes, scales)
+    _rows_2d("swiglu_quant x", x, torch.bfloat16)
+    rows, width = x.shape
+    if width % 2:
+        raise ValueError(f"swiglu_quant: row width {width} is not [gate | up]")
+    half = width // 2
+    if out is True:
+        out = torch.empty((rows, half), device=x.device, dtype=torch.bfloat16)
+    elif not want_out:
+        out = None
+    if out is not None:
+        _rows_2d("swiglu_quant out", out, torch.bfloat16)
+        if tuple(out.shape) != (rows, half):
+            raise ValueError("swiglu_quant: out shape mismatch")
+    if fmt is not None:
+        if codes is None:
+            codes = torch.empty((rows, half), device=x.device, dtype=_CODE_DTYPES[fmt])
+        if scales is None:
+            scales = torch.empty((rows, 1), device=x.device, dtype=torch.float32)
+        _rows_2d("swiglu_quant codes", codes, _CODE_DTYPES[fmt])
+        if tuple(codes.shape) != (rows, half):
+            raise ValueError("swiglu_quant: codes shape mismatch")
+        if scales.dtype != torch.float32 or scales.numel() != rows or not scales.is_contiguous():
+            raise ValueError("swiglu_quant: scales must be a contiguous fp32 tensor with one entry per row")
+    elif codes is not None or scales is not None:
+        raise ValueError("swiglu_quant: codes / scales given without a format")
+    if out is None and fmt is None:
+        raise ValueError("swiglu_quant: neither a bf16 output nor codes requested")
+    ld = lambda t, w: (t.stride(0) if rows > 1 else w) if t is not None else w
+    _lib.call("h3q_swiglu_quant", _ptr(x), ld(x, width), rows, half, _ptr(out), ld(out, half),
+              FMT_INT8 if fmt is None else fmt, rounding, _ptr(codes), ld(codes, half), _ptr(scales), _stream(x))
+    return out, codes, scales
+
+
 def quant_per_head_e4m3(x: torch.Tensor, *, codes: torch.Tensor | None = None, scales: torch.Tensor | None = None,
                         workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-(batch, head) e4m3fn of a bf16 ``x [B, S, H, D]``: (codes [B, S, H, D]
