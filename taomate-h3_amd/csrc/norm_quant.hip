@@ -57,6 +57,20 @@ __device__ __forceinline__ uint32_t words_of(const uint4& v, int j) {
     return j == 0 ? v.x : (j == 1 ? v.y : (j == 2 ? v.z : v.w));
 }
 
+// 16-byte vector `vec` of a buffer of nvec vectors; a lane past the end gets
+// an out-of-range offset and reads zeros.  No branch, so the compiler keeps
+// every load of a row in flight together (a load under a per-lane condition
+// is emitted as a masked load followed by a wait).
+__device__ __forceinline__ uint4 load16(__amdgpu_buffer_rsrc_t r, int vec, int nvec) {
+    const v4u w = __builtin_amdgcn_raw_buffer_load_b128(r, vec < nvec ? vec * 16 : (int)0x80000000u, 0, 0);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// The store counterpart: a lane past the end is dropped by the hardware.
+__device__ __forceinline__ void store16(__amdgpu_buffer_rsrc_t r, int vec, int nvec, const uint4& v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v4u{v.x, v.y, v.z, v.w}, r, vec < nvec ? vec * 16 : (int)0x80000000u, 0, 0);
+}
+
 }  // namespace
 
 template <int FMT, int ROUND, int NV, bool RESID>
@@ -64,54 +78,96 @@ __global__ __launch_bounds__(256) void norm_modulate_quant_kernel(NormQuantArgs 
     const int lane = threadIdx.x & 63;
     const int nvec = p.cols >> 3;
     const int64_t step = (int64_t)gridDim.x * 4;
-    for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < p.rows; row += step) {
-        const int64_t trow = p.indices[row];
-        const uint4* tab_scale = reinterpret_cast<const uint4*>(p.scale + trow * p.table_stride);
-        const uint4* tab_shift = reinterpret_cast<const uint4*>(p.shift + trow * p.table_stride);
-        const uint4* wv = reinterpret_cast<const uint4*>(p.weight);
+    // The row (and every buffer descriptor built from it) is wave-uniform;
+    // saying so keeps the descriptors in SGPRs (otherwise each buffer load
+    // is wrapped in a loop over the distinct descriptors of the wave).
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // The table rows of this wave's next 64 rows are read together (lane l
+    // holds that of row + l * step) and picked out with readlane, so a row's
+    // loads wait for no index load of their own.
+    int idx_lo = 0, idx_hi = 0;
+    int it = 0;
+    for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < p.rows; row += step, ++it) {
+        if ((it & 63) == 0) {
+            const int64_t r = row + (int64_t)lane * step;
+            const int64_t t = r < p.rows ? p.indices[r] : 0;
+            idx_lo = (int)(uint32_t)t;
+            idx_hi = (int)(t >> 32);
+        }
+        const int64_t trow = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane(idx_hi, it & 63) << 32) |
+                                       (uint32_t)__builtin_amdgcn_readlane(idx_lo, it & 63));
+        const uint32_t row_bytes = (uint32_t)nvec * 16u;
+        const __amdgpu_buffer_rsrc_t tab_scale = make_rsrc(p.scale + trow * p.table_stride, row_bytes);
+        const __amdgpu_buffer_rsrc_t tab_shift = make_rsrc(p.shift + trow * p.table_stride, row_bytes);
+        const __amdgpu_buffer_rsrc_t wv = make_rsrc(p.weight, row_bytes);
         uint4 v[NV];
         if constexpr (RESID) {
-            const uint4* rr = reinterpret_cast<const uint4*>(p.value + row * p.ldv);
-            const uint4* br = reinterpret_cast<const uint4*>(p.branch + row * p.ldb);
-            const uint4* gr = reinterpret_cast<const uint4*>(p.gate + trow * p.table_stride);
-            uint4* hr = reinterpret_cast<uint4*>(p.hidden + row * p.ldh);
+            const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.value + row * p.ldv, row_bytes);
+            const __amdgpu_buffer_rsrc_t br = make_rsrc(p.branch + row * p.ldb, row_bytes);
+            const __amdgpu_buffer_rsrc_t gr = make_rsrc(p.gate + trow * p.table_stride, row_bytes);
+            const __amdgpu_buffer_rsrc_t hr = make_rsrc(p.hidden + row * p.ldh, row_bytes);
+            // Batches of four vectors (twelve loads in flight).
+            constexpr int B = 4;
 #pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                const int vec = i * 64 + lane;
-                v[i] = make_uint4(0, 0, 0, 0);
-                if (vec < nvec) {
-                    const uint4 r = rr[vec], b = br[vec], g = gr[vec];
+            for (int i0 = 0; i0 < NV; i0 += B) {
+                uint4 r[B], b[B], g[B];
+#pragma unroll
+                for (int k = 0; k < B && i0 + k < NV; ++k) {
+                    const int vec = (i0 + k) * 64 + lane;
+                    r[k] = load16(rr, vec, nvec);
+                    b[k] = load16(br, vec, nvec);
+                    g[k] = load16(gr, vec, nvec);
+                }
+#pragma unroll
+                for (int k = 0; k < B && i0 + k < NV; ++k) {
+                    const int vec = (i0 + k) * 64 + lane;
                     uint32_t h[4];
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const uint32_t rw = words_of(r, j), bw = words_of(b, j), gw = words_of(g, j);
+                        const uint32_t rw = words_of(r[k], j), bw = words_of(b[k], j), gw = words_of(g[k], j);
                         const uint32_t gb = rb2(fmul(lo_f(gw), lo_f(bw)), fmul(hi_f(gw), hi_f(bw)));
                         h[j] = rb2(fadd(lo_f(rw), lo_f(gb)), fadd(hi_f(rw), hi_f(gb)));
                     }
-                    v[i] = make_uint4(h[0], h[1], h[2], h[3]);
-                    hr[vec] = v[i];
+                    // Past the row the inputs read as zeros, and 0 + bf16(0 * 0) = +0.
+                    v[i0 + k] = make_uint4(h[0], h[1], h[2], h[3]);
+                    store16(hr, vec, nvec, v[i0 + k]);
                 }
             }
         } else {
-            const uint4* xr = reinterpret_cast<const uint4*>(p.value + row * p.ldv);
+            const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.value + row * p.ldv, row_bytes);
 #pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                const int vec = i * 64 + lane;
-                v[i] = vec < nvec ? xr[vec] : make_uint4(0, 0, 0, 0);
-            }
+            for (int i = 0; i < NV; ++i) v[i] = load16(xr, i * 64 + lane, nvec);
         }
 
-        // Sum of squares in the fixed order, then the butterfly.
+        // Weight / scale / shift vectors in batches of TB, two batches in
+        // registers: batch 0 is requested with the row, batch b + 1 before
+        // batch b is used, so the table round trips overlap the arithmetic.
+        constexpr int TB = 2;
+        uint4 w[2][TB], sc[2][TB], sh[2][TB];
+        auto load_tables = [&](int i0, int slot) {
+#pragma unroll
+            for (int k = 0; k < TB; ++k) {
+                if (i0 + k < NV) {
+                    const int vec = (i0 + k) * 64 + lane;
+                    w[slot][k] = load16(wv, vec, nvec);
+                    sc[slot][k] = load16(tab_scale, vec, nvec);
+                    sh[slot][k] = load16(tab_shift, vec, nvec);
+                }
+            }
+        };
+        load_tables(0, 0);
+        __builtin_amdgcn_sched_barrier(0);  // issued here, not moved to their first use
+
+        // Sum of squares in the fixed order, then the butterfly.  Lanes past
+        // the row hold +0 (read as zeros above), and ss + (+0 * +0) = ss.
         float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            if (i * 64 + lane < nvec) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t w = words_of(v[i], j);
-                    ss = fadd(ss, fmul(lo_f(w), lo_f(w)));
-                    ss = fadd(ss, fmul(hi_f(w), hi_f(w)));
-                }
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t w = words_of(v[i], j);
+                ss = fadd(ss, fmul(lo_f(w), lo_f(w)));
+                ss = fadd(ss, fmul(hi_f(w), hi_f(w)));
             }
         }
 #pragma unroll
@@ -134,16 +190,22 @@ __global__ __launch_bounds__(256) void norm_modulate_quant_kernel(NormQuantArgs 
         // the table loads.
         uint32_t m = 0;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int vec = i * 64 + lane;
-            if (vec < nvec) {
-                const uint4 w = wv[vec], sc = tab_scale[vec], sh = tab_shift[vec];
+        for (int i0 = 0; i0 < NV; i0 += TB) {
+            const int slot = (i0 / TB) & 1;
+            if (i0 + TB < NV) load_tables(i0 + TB, slot ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < TB && i0 + k < NV; ++k) {
+                const int i = i0 + k;
+                // Past the row x, w, scale and shift are zeros; with rs = 0
+                // there y = bf16(bf16(0 * 1) + 0) = +0 even when rs is infinite.
+                const float rsi = i * 64 + lane < nvec ? rs : 0.0f;
                 uint32_t y[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const uint32_t xw = words_of(v[i], j), ww = words_of(w, j);
-                    const uint32_t cw = words_of(sc, j), hw = words_of(sh, j);
-                    const uint32_t nw = rb2(fmul(fmul(lo_f(xw), rs), lo_f(ww)), fmul(fmul(hi_f(xw), rs), hi_f(ww)));
+                    const uint32_t xw = words_of(v[i], j), ww = words_of(w[slot][k], j);
+                    const uint32_t cw = words_of(sc[slot][k], j), hw = words_of(sh[slot][k], j);
+                    const uint32_t nw = rb2(fmul(fmul(lo_f(xw), rsi), lo_f(ww)), fmul(fmul(hi_f(xw), rsi), hi_f(ww)));
                     const uint32_t s1 = rb2(fadd(1.0f, lo_f(cw)), fadd(1.0f, hi_f(cw)));
                     const uint32_t tw = rb2(fmul(lo_f(nw), lo_f(s1)), fmul(hi_f(nw), hi_f(s1)));
                     y[j] = rb2(fadd(lo_f(tw), lo_f(hw)), fadd(hi_f(tw), hi_f(hw)));
@@ -153,10 +215,9 @@ __global__ __launch_bounds__(256) void norm_modulate_quant_kernel(NormQuantArgs 
             }
         }
         if (p.out) {
-            uint4* orow = reinterpret_cast<uint4*>(p.out + row * p.ldo);
+            const __amdgpu_buffer_rsrc_t orow = make_rsrc(p.out + row * p.ldo, row_bytes);
 #pragma unroll
-            for (int i = 0; i < NV; ++i)
-                if (i * 64 + lane < nvec) orow[i * 64 + lane] = v[i];
+            for (int i = 0; i < NV; ++i) store16(orow, i * 64 + lane, nvec, v[i]);
         }
         if (p.codes == nullptr) continue;
 #pragma unroll
@@ -166,15 +227,12 @@ __global__ __launch_bounds__(256) void norm_modulate_quant_kernel(NormQuantArgs 
         const float amax = wave_max(amax_from_packed(m));
         RowQuant<FMT, ROUND> rq;
         rq.init(amax);
+        const __amdgpu_buffer_rsrc_t qrow = make_rsrc(p.codes + row * p.ldq, (uint32_t)nvec * 8u);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int vec = i * 64 + lane;
-            if (vec < nvec) {
-                uint2 out;
-                out.x = rq.pack4(v[i].x, v[i].y);
-                out.y = rq.pack4(v[i].z, v[i].w);
-                *reinterpret_cast<uint2*>(p.codes + row * p.ldq + 8 * (int64_t)vec) = out;
-            }
+            const v2u out = {rq.pack4(v[i].x, v[i].y), rq.pack4(v[i].z, v[i].w)};
+            __builtin_amdgcn_raw_buffer_store_b64(out, qrow, vec < nvec ? vec * 8 : (int)0x80000000u, 0, 0);
         }
         if (lane == 0) p.scales[row] = rq.s;
     }
