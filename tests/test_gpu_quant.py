@@ -99,8 +99,11 @@ def test_rows_extreme_magnitudes(ops, oracle, device, fmt, rounding):
     _check_rows(ops, oracle, x.to(torch.bfloat16), device, fmt, rounding)
 
 
+# Shapes include the c2 activations (8192 x 5120) and row counts past the
+# 1024-workgroup grid of the two passes (several rows per wave).
 @pytest.mark.parametrize("static", [False, True])
-@pytest.mark.parametrize("m,k", [(256, 1024), (1000, 5120), (3, 37), (4097, 8)])
+@pytest.mark.parametrize("m,k", [(256, 1024), (1000, 5120), (3, 37), (4097, 8), (8192, 5120), (9000, 256),
+                                 (8200, 5120), (16400, 64)])
 def test_tensor_e4m3_matches_oracle(ops, oracle, device, static, m, k):
     x = activations(m, k, seed=m + k, outlier_channels=max(1, k // 100))
     xb = bits16(x)
@@ -114,7 +117,7 @@ def test_tensor_e4m3_matches_oracle(ops, oracle, device, static, m, k):
 
 
 @pytest.mark.parametrize("static", [False, True])
-@pytest.mark.parametrize("m,k", [(1000, 5120), (3, 37)])
+@pytest.mark.parametrize("m,k", [(1000, 5120), (3, 37), (8192, 5120), (8200, 5120)])
 def test_tensor_e4m3_bf16_divisor_matches_oracle(ops, oracle, device, static, m, k):
     """The eager-on-GPU form (h3q_quant_tensor_e4m3_bf16_divisor): divisor
     bf16(s), returned scale s."""
