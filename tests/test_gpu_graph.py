@@ -1,0 +1,55 @@
+"""The act-quant + GEMM step captured in a HIP graph (as bench.py and a
+serving loop replay it): every replay, with eager work and synchronizations
+between replays and the captured input overwritten in place, gives the eager
+step's codes, scales and bf16 output bit for bit."""
+
+from __future__ import annotations
+
+import torch
+
+import pytest
+
+from _util import activations, bits16
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graph_replays_match_eager(ops, device):
+    m, k, n = 512, 1024, 768
+    gen = torch.Generator().manual_seed(21)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    bias = torch.randn(n, generator=gen).to(torch.bfloat16).to(device)
+    q_w, s_w = ops.quant_rows_tiled(w, ops.FMT_E4M3FN)
+    s_w = s_w.reshape(-1)
+    x = activations(m, k, seed=22).to(device)
+    q_a = torch.empty(m, k, device=device, dtype=torch.float8_e4m3fn)
+    s_a = torch.empty(m, 1, device=device, dtype=torch.float32)
+    out = torch.empty(m, n, device=device, dtype=torch.bfloat16)
+
+    def step():
+        ops.quant_rows(x, ops.FMT_E4M3FN, codes=q_a, scales=s_a)
+        ops.scaled_mm(q_a, q_w, s_a.reshape(-1), s_w, bias=bias, out=out, b_tiled=True)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+
+    for replay in range(4):
+        print(f"graph replay {replay}", flush=True)
+        x.copy_(activations(m, k, seed=100 + replay).to(device))
+        # eager reference on separate buffers, then the replay on the captured ones
+        rq, rs = ops.quant_rows(x, ops.FMT_E4M3FN)
+        ref = ops.scaled_mm(rq, q_w, rs.reshape(-1), s_w, bias=bias, b_tiled=True)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(q_a.view(torch.uint8), rq.view(torch.uint8))
+        assert torch.equal(s_a.reshape(-1), rs.reshape(-1))
+        assert (bits16(out) == bits16(ref)).all()
