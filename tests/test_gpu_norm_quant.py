@@ -178,3 +178,10 @@ def test_full_size_hidden_5376(ops, oracle, device):
     """The real H3 hidden width (TP-local K = 5376) at 1312 tokens (480p,
     phase 0), int8 codes for the QKV linear."""
     _check(ops, oracle, device, 1312, 5376, "int8", "rcp", True, t=6, seed=77, want_out=False)
+
+
+def test_more_than_64_rows_per_wave(ops, oracle, device):
+    """Past 64 * 4096 rows a wave handles more than 64 rows and re-reads the
+    table indices of its next 64 rows; random indices over five table rows
+    make a misplaced index visible."""
+    _check(ops, oracle, device, 64 * 4096 + 37, 8, "int8", "rcp", resid=True, t=5, seed=11)
