@@ -316,6 +316,7 @@ ORC_API void orc_quant_tensor_e4m3(const uint16_t* x, int64_t rows, int64_t k, i
 /* acc[m][n] = sum_k a[m][k] * b[n][k], exact in int32 (|acc| <= K*128^2). */
 ORC_API void orc_gemm_i8_i32(const int8_t* a, int64_t lda, const int8_t* b, int64_t ldb,
                              int32_t* c, int64_t ldc, int64_t m, int64_t n, int64_t k) {
+#pragma omp parallel for collapse(2) schedule(static)
     for (int64_t i = 0; i < m; ++i)
         for (int64_t j = 0; j < n; ++j) {
             int64_t acc = 0;

@@ -17,7 +17,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libtaomate_h3_amd.so"
-SOURCES = ["act_quant.hip", "head_quant.hip", "norm_quant.hip", "swiglu_quant.hip", "gemm.hip", "gemm_skinny.hip", "capi.hip"]
+SOURCES = ["act_quant.hip", "head_quant.hip", "norm_quant.hip", "swiglu_quant.hip", "gemm.hip", "gemm_w4.hip", "gemm_skinny.hip", "capi.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -302,6 +302,9 @@ static int check_gemm_operands(const char* who, const void* a, int64_t lda, cons
         return fail(H3Q_ERR_UNSUPPORTED, "%s: row stride above 8 MiB", who);
     if ((m + 255) / 256 * ((n + 255) / 256) >= (int64_t(1) << 31))
         return fail(H3Q_ERR_UNSUPPORTED, "%s: too many output tiles", who);
+    // A 256-row tile of a tiled operand spans 256 * k bytes behind a 32-bit offset.
+    if ((a_tiled || b_tiled) && 256 * k >= (int64_t(1) << 31))
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: tiled operands need 256 * k below 2^31", who);
     return H3Q_OK;
 }
 
@@ -320,9 +323,7 @@ __attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void*
             return fail(H3Q_ERR_INVALID, "%s: unknown operand layout %d", who, layout);
     const bool a_tiled = a_layout == H3Q_LAYOUT_TILED, b_tiled = b_layout == H3Q_LAYOUT_TILED;
     if (int rc = check_gemm_operands(who, a, lda, b, ldb, m, n, k, 1, a_tiled, b_tiled)) return rc;
-    if (a_tiled && (m > h3q::kSkinnyMaxM || lora_t))
-        return fail(H3Q_ERR_UNSUPPORTED, "%s: tiled activations need m <= %lld and no LoRA", who,
-                    (long long)h3q::kSkinnyMaxM);
+    if (a_tiled && lora_t) return fail(H3Q_ERR_UNSUPPORTED, "%s: tiled activations take no LoRA epilogue", who);
     for (int kind : {a_scale_kind, b_scale_kind})
         if (kind != H3Q_SCALE_PER_ROW && kind != H3Q_SCALE_PER_TENSOR)
             return fail(H3Q_ERR_INVALID, "%s: unknown scale kind %d", who, kind);
@@ -338,7 +339,17 @@ __attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void*
         if (ldt < lora_rank || ldlb < lora_rank || ldt % 8 || ldlb % 8 || !aligned(lora_t, 16) ||
             !aligned(lora_b, 16))
             return fail(H3Q_ERR_INVALID, "%s: LoRA operands must be 16-byte aligned rows of >= rank", who);
+        // 256 rows of either LoRA operand sit behind a 32-bit buffer offset.
+        if (ldt * 2 >= (int64_t(1) << 23) || ldlb * 2 >= (int64_t(1) << 23))
+            return fail(H3Q_ERR_UNSUPPORTED, "%s: LoRA row stride above 8 MiB", who);
     }
+    // Tiled activations beyond the weight-streaming GEMM's rows are read by the
+    // four-wave GEMM only (see w4_supported).
+    if (a_tiled && m > h3q::kSkinnyMaxM && (k < 256 || n % 8 || ldo % 8 || !aligned(out, 16)))
+        return fail(H3Q_ERR_UNSUPPORTED,
+                    "%s: tiled activations with m > %lld need k >= 256, n and ldo multiples of 8 and a 16-byte "
+                    "aligned output",
+                    who, (long long)h3q::kSkinnyMaxM);
     if (m == 0 || n == 0) return ok();
     if (!a || !b || !a_scale || !b_scale || !out) return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
     h3q::GemmArgs g{};

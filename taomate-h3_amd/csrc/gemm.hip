@@ -34,6 +34,7 @@
 //   bf16 GEMM:   bf16(acc)
 #include "h3q_common.hpp"
 #include "h3q_kernels.hpp"
+#include "gemm_tiles.hpp"
 
 namespace h3q {
 
@@ -200,35 +201,7 @@ __device__ __forceinline__ void mma_stage(const H3Q_LDS uint8_t* sa, const H3Q_L
     }
 }
 
-// Logical tile of block index bid.  Workgroups are dealt to the 8 XCDs round
-// robin (XCD = blockIdx % 8); give each XCD a contiguous run of tiles so the
-// tiles resident on one XCD share A and B rows in that XCD's L2.  Within the
-// run, tiles go column-major in groups of kGroupM tile-rows.  A persistent
-// grid passes bid = blockIdx + j * gridDim with gridDim % 8 == 0, which keeps
-// bid % 8 equal to the XCD the workgroup runs on.
-__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
-    constexpr int kXcds = 8, kGroupM = 8;
-    const int total = tiles_m * tiles_n;
-    const int q = total / kXcds, rem = total % kXcds;
-    const int xcd = bid % kXcds, local = bid / kXcds;
-    const int t = xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
-    const int per_group = kGroupM * tiles_n;
-    const int group = t / per_group;
-    const int first_m = group * kGroupM;
-    const int gsize = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
-    const int in_group = t - group * per_group;
-    tm = first_m + in_group % gsize;
-    tn = in_group / gsize;
-}
-
 enum Epi : int { kEpiScaled = 0, kEpiI32 = 1, kEpiBF16 = 2 };
-
-// Workgroup barrier for the copy ring.  __syncthreads() would add a release
-// fence, which waits for every in-flight LDS copy (vmcnt(0)) and so drains the
-// ring; here the caller has already waited for exactly the stage it needs, and
-// only this wave's LDS reads must be complete before others overwrite a
-// buffer.  The asm memory clobber keeps LDS accesses on their side.
-__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Wait until the oldest `pending + 1` copy stages of this wave have landed,
 // leaving `pending` younger stages in flight (only used while draining).
@@ -427,15 +400,6 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
     }
 }
 
-// Lane index that the compiler cannot hoist out of a loop: recomputing
-// lane-derived offsets inside each tile iteration keeps them from staying
-// live (in registers) across the epilogue of the persistent kernel.
-__device__ __forceinline__ int opaque_lane() {
-    int l;
-    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-    return l;
-}
-
 // Persistent scaled GEMM (e4m3 / int8 -> bf16, optional bias, no LoRA, 4-column
 // stores).  A grid of at most one workgroup per CU walks the output tiles
 // blockIdx.x, blockIdx.x + gridDim.x, ... with one continuous 2-stage copy
@@ -622,21 +586,6 @@ hipError_t launch_tile(const GemmArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-// Workgroups of the persistent GEMM: one per CU of the current device (the
-// LDS ring allows one per CU), rounded down to a multiple of the 8 XCDs.
-static int persistent_grid(int tiles) {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    int cus = dev < 64 ? __atomic_load_n(&cached[dev], __ATOMIC_RELAXED) : 0;
-    if (cus == 0) {
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8) cus = 8;
-        if (dev < 64) __atomic_store_n(&cached[dev], cus, __ATOMIC_RELAXED);
-    }
-    cus -= cus % 8;
-    return tiles < cus ? tiles : cus;
-}
-
 template <class T, int OP, bool BIAS>
 hipError_t launch_persistent(const GemmArgs& a, hipStream_t st) {
     const int tiles_m = (int)((a.m + T::BM - 1) / T::BM), tiles_n = (int)((a.n + T::BN - 1) / T::BN);
@@ -683,6 +632,7 @@ hipError_t launch_gemm(int kind, bool raw_i32, const GemmArgs& args, hipStream_t
     a.out_vec = (a.ldo % 4 == 0) && (a.n % 4 == 0) && ((uintptr_t)a.out % 16 == 0);
     const bool lora = a.lora_t != nullptr;
     if (kind != kOpBF16 && !raw_i32 && skinny_supported(a)) return launch_gemm_skinny(kind, a, st);
+    if (kind != kOpBF16 && !raw_i32 && w4_supported(a)) return launch_gemm_w4(kind, a, st);
     if (kind == kOpE4M3)
         return lora ? launch_scaled<TileBigLora, kOpE4M3, true>(a, st) : launch_scaled<TileBig, kOpE4M3, false>(a, st);
     if (kind == kOpInt8) {

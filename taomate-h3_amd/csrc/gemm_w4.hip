@@ -1,0 +1,428 @@
+// Persistent scaled GEMM for large M on gfx950: four waves of 128 x 128.
+//
+//   out[m, n] = bf16( s_a[m] * (s_w[n] * float(sum_k A[m, k] * B[n, k])) [+ bias[n]] )
+//
+// A workgroup of four waves (one per SIMD) walks 256 x 256 output tiles
+// blockIdx.x, blockIdx.x + gridDim.x, ... (one workgroup per CU).  Each wave
+// owns a 128 x 128 block: 4 x 4 accumulators of the 32 x 32 MFMA
+// (v_mfma_f32_32x32x64_f8f6f4 / v_mfma_i32_32x32x32_i8), 256 registers that
+// live in the AGPR file for the whole kernel.  Per output element the MFMA
+// pipe then needs half the LDS fragment reads of 64 x 64 wave blocks.
+//
+// K advances in 64-byte steps through a ring of four 32 KiB LDS stages
+// (A 256 x 64 and B 256 x 64 codes each), filled by buffer_load_dwordx4 ...
+// lds.  Step u (one per k-step, continuous across the tiles of a workgroup):
+//   * 16 MFMAs (int8: 32) on the fragments of stage u, held in registers;
+//   * the fragments of stage u + 1 read into the other register set;
+//   * the 8 copy instructions of step u + 4 into stage u, which every wave
+//     finished reading (into registers) before the barrier that ended step
+//     u - 1;
+//   * wait until the copies of step u + 2 have landed (vmcnt <= 16), barrier.
+// A copy is thus issued two to three steps before it is read.
+//
+// Operand layouts in the stages:
+//   * row-major (lda / ldb bytes per row): a row's 64 bytes are 4 chunks of
+//     16, chunk c at c ^ swz(row), so the ds_read_b128 of 16 consecutive rows
+//     at one chunk hit distinct banks;
+//   * tiled (16-row x 128-byte blocks of 2 KiB in fragment order, see
+//     include/taomate_h3_amd.h): a 64-byte step of a block is two 512-byte
+//     pieces 1 KiB apart, copied as one 1 KiB wave instruction and read in
+//     place (16 consecutive rows read 16 consecutive 16-byte slots).
+//
+// The per-row / per-column scale vectors and the bias of a tile are copied
+// into LDS (double-buffered by tile parity) together with the tile's first
+// k-step.  Their extra copy instruction makes some waits cover one more
+// load than needed, never one less.
+//
+// Wait counts.  vmcnt counts loads and stores together.  Loads complete in
+// issue order among themselves, so with two newer load groups (16 loads)
+// outstanding behind the group a step needs, vmcnt <= 16 implies that group
+// has landed whatever the pending epilogue stores do: stores only make the
+// wait longer.
+//
+// Epilogue of a tile: the accumulators are read from the AGPRs, scaled in
+// the reference order s_a * (s_w * acc) (fma with the bias), rounded to bf16,
+// and staged per 32-row block through the ring stage whose contents the
+// next step's fragments already hold in registers; each store then writes
+// 4 rows x 256 contiguous bytes.  A barrier keeps copies out of that stage
+// until every wave has read it back.
+//
+// The MFMAs are inline asm with their accumulator operand pinned to AGPRs
+// ("a"); reading them back uses v_accvgpr_read after explicit wait states
+// for the MFMA's passes.  Results are the bits of gemm_kernel / the
+// persistent 16-wave kernel: the same instructions on the same operands in
+// the same k order.
+#include <stdint.h>
+
+#include "gemm_tiles.hpp"
+#include "h3q_common.hpp"
+#include "h3q_kernels.hpp"
+
+namespace h3q {
+
+namespace {
+
+constexpr int kW4Stages = 4;
+constexpr int kW4StageBytes = (256 + 256) * 64;  // 32 KiB
+constexpr int kW4ABytes = 256 * 64;              // A part of a stage
+
+// One wave copy (buffer_load_dwordx4 ... lds) with a scalar offset: lane L's
+// 16 bytes at src + voff + soff land at LDS byte lds_base + 16 L.  Inline
+// asm for the reason given at copy16 (h3q_common.hpp).
+__device__ __forceinline__ void copy16_soff(const CopySrc& src, uint32_t lds_base, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(src.d), "s"(soff)
+                 : "memory");
+}
+
+// MFMAs with the accumulator in AGPRs.  *_first starts a tile (srcC = 0).
+__device__ __forceinline__ void mfma_e4m3(v16f& c, const v8i& b, const v8i& a) {
+    asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, %0" : "+a"(c) : "v"(b), "v"(a));
+}
+__device__ __forceinline__ void mfma_e4m3_first(v16f& c, const v8i& b, const v8i& a) {
+    asm volatile("v_mfma_f32_32x32x64_f8f6f4 %0, %1, %2, 0" : "=a"(c) : "v"(b), "v"(a));
+}
+__device__ __forceinline__ void mfma_i8(v16i& c, const v4i& b, const v4i& a) {
+    asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+a"(c) : "v"(b), "v"(a));
+}
+__device__ __forceinline__ void mfma_i8_first(v16i& c, const v4i& b, const v4i& a) {
+    asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0" : "=a"(c) : "v"(b), "v"(a));
+}
+__device__ __forceinline__ float agpr_read(float x) {
+    float v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(x));
+    return v;
+}
+__device__ __forceinline__ float agpr_read(int x) {
+    int v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(x));
+    return (float)v;
+}
+
+// Chunk swizzle of a 64-byte row-major stage row (conflict-free ds_read_b128
+// of 16 consecutive rows at one logical chunk).
+__device__ __forceinline__ int swz64(int r) { return (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2); }
+
+template <int OP>
+struct W4Op;
+template <>
+struct W4Op<kOpE4M3> {
+    using acc_t = v16f;
+    using frag_t = v8i;
+    static constexpr int kSteps = 1;  // MFMA k-steps per 64-byte stage
+};
+template <>
+struct W4Op<kOpInt8> {
+    using acc_t = v16i;
+    using frag_t = v4i;
+    static constexpr int kSteps = 2;
+};
+
+}  // namespace
+
+template <int OP, bool BIAS, bool TA, bool TB>
+__global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m, int tiles_n) {
+    using acc_t = typename W4Op<OP>::acc_t;
+    using frag_t = typename W4Op<OP>::frag_t;
+    constexpr int KS = W4Op<OP>::kSteps;
+    constexpr int NM = 16 * KS;                   // MFMAs per step per wave
+    constexpr int NR = OP == kOpE4M3 ? 8 : 16;    // fragment reads (of 1 or 2 ds_read_b128) per step
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_ring[kW4Stages * kW4StageBytes];
+    // Per tile parity: row scales [256] f32 | column scales [256] f32 | bias [256] bf16.
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_ep[2 * 3 * 1024];
+    H3Q_LDS uint8_t* const ring = (H3Q_LDS uint8_t*)lds_ring;
+    H3Q_LDS uint8_t* const ep = (H3Q_LDS uint8_t*)lds_ep;
+    const uint32_t ring_addr = (uint32_t)(uintptr_t)ring;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm0 = (wave >> 1) * 128, wn0 = (wave & 1) * 128;
+    const int g = lane >> 5, c32 = lane & 31;
+    const int ksteps = (int)(p.k / 64);          // even: k % 128 == 0
+    const int64_t steps128 = p.k / 128;          // tiled operands: 128-byte k-steps per block row
+    const int ntiles = (tiles_m * tiles_n - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const bool row_scales = p.a_scale_per_row != 0, col_scales = p.b_scale_per_col != 0;
+    // A per-tensor scale fills its vector (both parities) once.
+    if (!row_scales || !col_scales) {
+        const float sa0 = row_scales ? 0.0f : p.a_scale[0], sw0 = col_scales ? 0.0f : p.b_scale[0];
+        for (int c = threadIdx.x; c < 2 * 256; c += 256) {
+            H3Q_LDS float* e = (H3Q_LDS float*)(ep + (c >> 8) * 3072);
+            if (!row_scales) e[c & 255] = sa0;
+            if (!col_scales) e[256 + (c & 255)] = sw0;
+        }
+    }
+
+    struct TileSrc {
+        int m0, n0, rows, cols;
+    };
+    auto tile_src = [&](int j) {
+        int tm, tn;
+        tile_coords((int)blockIdx.x + j * (int)gridDim.x, tiles_m, tiles_n, tm, tn);
+        TileSrc t;
+        t.m0 = tm * 256;
+        t.n0 = tn * 256;
+        t.rows = (int)(p.m - t.m0 < 256 ? p.m - t.m0 : 256);
+        t.cols = (int)(p.n - t.n0 < 256 ? p.n - t.n0 : 256);
+        return t;
+    };
+
+    // ---------------------------------------------------------------- copies
+    // Descriptors and per-lane offsets of the tile being fetched; the k-step
+    // enters as the scalar offset.  Past the last tile the descriptors are
+    // empty, so the trailing copies read zeros into stages nobody reads.
+    CopySrc ra(nullptr, 0), rb(nullptr, 0);
+    uint32_t voff_a[4], voff_b[4];
+    int cj = 0, cs = 0;  // tile / k-step of the next copy group
+    auto operand_offset = [&](bool tiled, int c, int sub_row, int pos, int ln, int rows, int64_t ld) -> uint32_t {
+        if (tiled) {  // 16-row block c
+            const int nblk = (rows + 15) / 16;
+            return c < nblk ? (uint32_t)(c * steps128 * 2048) + (uint32_t)((ln >> 5) * 1024 + (ln & 31) * 16)
+                            : 0x80000000u;
+        }
+        const int row = c * 16 + sub_row;  // 16 rows x 64 bytes per copy
+        return row < rows ? (uint32_t)row * (uint32_t)ld + (uint32_t)((pos ^ swz64(sub_row)) * 16) : 0x80000000u;
+    };
+    auto setup_copy_tile = [&](int j) {
+        const bool live = j < ntiles;
+        const TileSrc t = tile_src(live ? j : ntiles - 1);
+        const uint32_t a_bytes = TA ? (uint32_t)((t.rows + 15) / 16 * steps128 * 2048) : (uint32_t)((int64_t)t.rows * p.lda);
+        const uint32_t b_bytes = TB ? (uint32_t)((t.cols + 15) / 16 * steps128 * 2048) : (uint32_t)((int64_t)t.cols * p.ldb);
+        ra = CopySrc((const uint8_t*)p.a + (TA ? (int64_t)(t.m0 / 16) * steps128 * 2048 : (int64_t)t.m0 * p.lda),
+                     live ? a_bytes : 0u);
+        rb = CopySrc((const uint8_t*)p.b + (TB ? (int64_t)(t.n0 / 16) * steps128 * 2048 : (int64_t)t.n0 * p.ldb),
+                     live ? b_bytes : 0u);
+        const int ln = opaque_lane();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = wave + 4 * i;
+            voff_a[i] = operand_offset(TA, c, ln >> 2, ln & 3, ln, t.rows, p.lda);
+            voff_b[i] = operand_offset(TB, c, ln >> 2, ln & 3, ln, t.cols, p.ldb);
+        }
+    };
+    // Epilogue vectors of tile j into LDS (waves 0, 1, 2: one copy each).
+    auto issue_vectors = [&](int j) {
+        if (j >= ntiles) return;
+        const TileSrc t = tile_src(j);
+        H3Q_LDS uint8_t* e = ep + (j & 1) * 3072;
+        if (wave == 0 && row_scales)
+            copy16(CopySrc(p.a_scale + t.m0, (uint32_t)t.rows * 4u), (uint32_t)(uintptr_t)e, 16u * lane);
+        if (wave == 1 && col_scales)
+            copy16(CopySrc(p.b_scale + t.n0, (uint32_t)t.cols * 4u), (uint32_t)(uintptr_t)(e + 1024), 16u * lane);
+        if (BIAS && wave == 2)
+            copy16(CopySrc(p.bias + t.n0, (uint32_t)t.cols * 2u), (uint32_t)(uintptr_t)(e + 2048),
+                   lane < 32 ? 16u * lane : 0x80000000u);
+    };
+    // Copy q (0..3: A, 4..7: B) of the group for (cj, cs) into stage st.
+    auto issue_copy = [&](int q, int st) {
+        const uint32_t base = ring_addr + (uint32_t)(st * kW4StageBytes);
+        const uint32_t soff_t = (uint32_t)((cs >> 1) * 2048 + (cs & 1) * 512), soff_r = (uint32_t)(cs * 64);
+        if (q < 4)
+            copy16_soff(ra, base + (uint32_t)((wave + 4 * q) * 1024), voff_a[q], TA ? soff_t : soff_r);
+        else
+            copy16_soff(rb, base + (uint32_t)(kW4ABytes + (wave + 4 * (q - 4)) * 1024), voff_b[q - 4],
+                        TB ? soff_t : soff_r);
+    };
+    auto advance_copy = [&]() {
+        if (++cs == ksteps) {
+            cs = 0;
+            ++cj;
+            setup_copy_tile(cj);
+            issue_vectors(cj);
+        }
+    };
+
+    // ------------------------------------------------------ fragment reads
+    // Stage-relative byte offsets of this lane's fragment halves: rows
+    // wm0 + c32 (A) and wn0 + c32 (B) of the first 32-row block; block i adds
+    // 2048 in either layout.  e4m3: halves h = 0, 1 of the 32-byte fragment
+    // (k bytes 32 g + 16 h); int8: k-steps s = 0, 1 (k bytes 32 s + 16 g).
+    uint32_t rda[2], rdb[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int chunk = OP == kOpE4M3 ? 2 * g + h : 2 * h + g;      // logical 16-byte chunk of the row
+        const int tiled_off = ((c32 & 15) + 16 * (OP == kOpE4M3 ? g : h)) * 16 + (OP == kOpE4M3 ? h : g) * 512;
+        rda[h] = TA ? (uint32_t)(((wm0 + c32) >> 4) * 1024 + tiled_off)
+                    : (uint32_t)((wm0 + c32) * 64 + ((chunk ^ swz64(c32)) << 4));
+        rdb[h] = kW4ABytes + (TB ? (uint32_t)(((wn0 + c32) >> 4) * 1024 + tiled_off)
+                                 : (uint32_t)((wn0 + c32) * 64 + ((chunk ^ swz64(c32)) << 4)));
+    }
+    struct Frags {
+        frag_t a[4 * KS], b[4 * KS];
+    };
+    auto ld16 = [&](const H3Q_LDS uint8_t* ptr) -> v4i { return *(const H3Q_LDS v4i*)ptr; };
+    // Fragment x of stage st (e4m3: a0..a3, b0..b3; int8: a[i + 4 s], b[i + 4 s]).
+    auto read_frag = [&](Frags& F, int x, int st) {
+        const H3Q_LDS uint8_t* sb = ring + st * kW4StageBytes;
+        if constexpr (OP == kOpE4M3) {
+            const int y = x & 3;
+            const uint32_t* off = x < 4 ? rda : rdb;
+            const v8i f = __builtin_shufflevector(ld16(sb + off[0] + y * 2048), ld16(sb + off[1] + y * 2048), 0, 1, 2,
+                                                  3, 4, 5, 6, 7);
+            if (x < 4) F.a[y] = f;
+            else F.b[y] = f;
+        } else {
+            const int y = x & 3, s = (x & 7) >> 2;
+            const v4i f = ld16(sb + (x < 8 ? rda[s] : rdb[s]) + y * 2048);
+            if (x < 8) F.a[y + 4 * s] = f;
+            else F.b[y + 4 * s] = f;
+        }
+    };
+
+    acc_t acc[4][4];
+    Frags F0, F1;
+    // MFMA t of a step: acc[i][j] += b-fragment j x a-fragment i (k-step s).
+    auto mfma = [&](bool first, const Frags& Fc, int t) {
+        const int s = t / 16, i = (t % 16) / 4, j = t % 4;
+        if constexpr (OP == kOpE4M3) {
+            if (first) mfma_e4m3_first(acc[i][j], Fc.b[j], Fc.a[i]);
+            else mfma_e4m3(acc[i][j], Fc.b[j], Fc.a[i]);
+        } else {
+            if (first && s == 0) mfma_i8_first(acc[i][j], Fc.b[j + 4 * s], Fc.a[i + 4 * s]);
+            else mfma_i8(acc[i][j], Fc.b[j + 4 * s], Fc.a[i + 4 * s]);
+        }
+    };
+    // One step's instruction stream: every MFMA is followed by the next
+    // fragment read (first NR slots) or copy (next 8 slots), each slot kept
+    // in place by a scheduling barrier.
+    auto body = [&](bool first, const Frags& Fc, Frags& Fn, int rst, int cst) {
+#pragma unroll
+        for (int t = 0; t < NM; ++t) {
+            mfma(first, Fc, t);
+            if (t < NR) read_frag(Fn, t, rst);
+            else if (t - NR < 8) issue_copy(t - NR, cst);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // ------------------------------------------------------------- epilogue
+    auto epilogue = [&](int mj, int st) {
+        const TileSrc cur = tile_src(mj);
+        const int ln = opaque_lane();
+        const int gg = ln >> 5, cc = ln & 31;
+        const H3Q_LDS uint8_t* e = ep + (mj & 1) * 3072;
+        H3Q_LDS uint8_t* const scratch = ring + st * kW4StageBytes + wave * 8192;
+        const __amdgpu_buffer_rsrc_t ro =
+            make_rsrc((uint8_t*)p.out + (int64_t)cur.m0 * p.ldo * 2, (uint32_t)((int64_t)cur.rows * p.ldo * 2));
+        // This lane's vectors, read once (before any scratch write): row
+        // scales of rows wm0 + 32 i + cc; column scales and bias of columns
+        // wn0 + 8 g16 + 4 gg + x, g16 = 4 jj + q.
+        float sa[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sa[i] = ((const H3Q_LDS float*)e)[wm0 + 32 * i + cc];
+        v4f sw4[16];
+        v2u b4[16];
+#pragma unroll
+        for (int g16 = 0; g16 < 16; ++g16) {
+            const int nl = wn0 + 8 * g16 + 4 * gg;
+            sw4[g16] = *(const H3Q_LDS v4f*)(e + 1024 + 4 * nl);
+            if constexpr (BIAS) b4[g16] = *(const H3Q_LDS v2u*)(e + 2048 + 2 * nl);
+        }
+        // Store columns of this lane: 8 bf16 at wn0 + 8 (ln % 16).
+        const int col8 = wn0 + 8 * (ln & 15);
+        const bool col_ok = col8 < cur.cols;
+        // VALU reads of MFMA results: wait out the last MFMAs' passes.
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int g16 = 0; g16 < 16; ++g16) {
+                const int jj = g16 >> 2, q = g16 & 3;
+                float y[4];
+#pragma unroll
+                for (int x = 0; x < 4; ++x) {
+                    const float t = __fmul_rn(sw4[g16][x], agpr_read(acc[i][jj][4 * q + x]));
+                    if constexpr (BIAS) {
+                        const uint32_t w = b4[g16][x >> 1];
+                        y[x] = __builtin_fmaf(sa[i], t, (x & 1) ? bf16_hi(w) : bf16_lo(w));
+                    } else {
+                        y[x] = __fmul_rn(sa[i], t);
+                    }
+                }
+                // row cc of the block, columns 8 g16 + 4 gg .. + 3 of the wave
+                *(H3Q_LDS v2u*)(scratch + cc * 256 + ((g16 ^ (cc & 15)) << 4) + gg * 8) =
+                    v2u{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+            }
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const int row = 4 * r + (ln >> 4);
+                const v4u v = *(const H3Q_LDS v4u*)(scratch + row * 256 + (((ln & 15) ^ (row & 15)) << 4));
+                const uint32_t off =
+                    col_ok ? ((uint32_t)(wm0 + 32 * i + row) * (uint32_t)p.ldo + (uint32_t)(cur.n0 + col8)) * 2u
+                           : 0xFFFFFFF0u;
+                __builtin_amdgcn_raw_buffer_store_b128(v, ro, off, 0, 0);
+            }
+        }
+    };
+
+    // ------------------------------------------------------------ main loop
+    setup_copy_tile(0);
+    issue_vectors(0);
+#pragma unroll
+    for (int st = 0; st < kW4Stages; ++st) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) issue_copy(q, st);
+        advance_copy();
+    }
+    wait_vmcnt<(kW4Stages - 1) * 8>();
+    ring_barrier();
+#pragma unroll
+    for (int x = 0; x < NR; ++x) read_frag(F0, x, 0);
+    wait_vmcnt<(kW4Stages - 2) * 8>();
+    ring_barrier();
+
+    int cur_st = 0;  // stage of the running step (its fragments are in registers)
+    auto step = [&](bool first, const Frags& Fc, Frags& Fn) {
+        const int nxt_st = cur_st + 1 == kW4Stages ? 0 : cur_st + 1;
+        body(first, Fc, Fn, nxt_st, cur_st);
+        advance_copy();
+        wait_vmcnt<(kW4Stages - 2) * 8>();
+        ring_barrier();
+        cur_st = nxt_st;
+    };
+    for (int mj = 0; mj < ntiles; ++mj) {
+        step(true, F0, F1);
+        step(false, F1, F0);
+        for (int s = 2; s < ksteps; s += 2) {
+            step(false, F0, F1);
+            step(false, F1, F0);
+        }
+        // Stage cur_st is free until the next step's copies: stage through it.
+        epilogue(mj, cur_st);
+        ring_barrier();
+    }
+    wait_vmcnt<0>();
+}
+
+bool w4_supported(const GemmArgs& a) {
+    // k in 128-byte steps (at least two, so each tile spans four ring stages),
+    // 8-column bf16 stores, a 16-byte aligned output, and the 32-bit
+    // block-relative offsets of the copies and stores.
+    if (a.lora_t || a.k % 128 || a.k < 256 || a.n % 8 || a.ldo % 8 || (uintptr_t)a.out % 16) return false;
+    if (a.m <= kSkinnyMaxM) return false;
+    const int64_t tiled_block_row = (a.k / 128) * 2048 * 16;  // 256 rows of a tiled operand
+    if ((a.a_tiled && tiled_block_row >= (int64_t(1) << 31)) || (a.b_tiled && tiled_block_row >= (int64_t(1) << 31)))
+        return false;
+    return 256 * a.ldo * 2 < (int64_t(1) << 31);
+}
+
+template <int OP, bool BIAS>
+static hipError_t launch_w4_op(const GemmArgs& a, hipStream_t st) {
+    const int tiles_m = (int)((a.m + 255) / 256), tiles_n = (int)((a.n + 255) / 256);
+    const dim3 grid((unsigned)persistent_grid(tiles_m * tiles_n));
+    if (a.a_tiled) {
+        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+    } else {
+        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_w4(int kind, const GemmArgs& a, hipStream_t st) {
+    if (kind == kOpE4M3) return a.bias ? launch_w4_op<kOpE4M3, true>(a, st) : launch_w4_op<kOpE4M3, false>(a, st);
+    return a.bias ? launch_w4_op<kOpInt8, true>(a, st) : launch_w4_op<kOpInt8, false>(a, st);
+}
+
+}  // namespace h3q

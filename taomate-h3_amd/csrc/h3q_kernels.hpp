@@ -76,6 +76,13 @@ struct GemmArgs {
 // kOpBF16: plain bf16 GEMM (LoRA down-projection).
 hipError_t launch_gemm(int kind, bool raw_i32, const GemmArgs& args, hipStream_t st);
 
+// Persistent four-wave GEMM for large M (gemm_w4.hip): scaled e4m3 / int8 ->
+// bf16 with optional bias, no LoRA; row-major or tiled A and B; k % 128 == 0,
+// k >= 256, n % 8 == 0, ldo % 8 == 0, 16-byte aligned output, m > kSkinnyMaxM.
+// launch_gemm routes there itself when w4_supported() holds.
+bool w4_supported(const GemmArgs& a);
+hipError_t launch_gemm_w4(int kind, const GemmArgs& a, hipStream_t st);
+
 // Weight-streaming GEMM for M <= kSkinnyMaxM activation rows (scaled e4m3 /
 // int8 to bf16, optional bias, no LoRA).  launch_gemm routes there itself.
 constexpr int64_t kSkinnyMaxM = 128;

@@ -275,7 +275,7 @@ def quantize_h3_block_linears_fp8_w8a8_(torch: Any, transformer: Any, *, policy:
     for the selected block linears (no counterpart in the reference; the
     format of the BASELINE FP8 W8A8 configurations).  Bias is kept (bf16) and
     fused into the GEMM epilogue.  Weights with N % 16 == 0 and K % 128 == 0
-    are stored in the tiled layout (``weight._h3q_tiled``)."""
+    are stored in the tiled layout (``ops.is_tiled(weight)``)."""
     candidates = _block_candidates(transformer, (".attn.qkv_proj", ".attn.out_proj", ".mlp.fc1", ".mlp.fc2"))
     if not candidates:
         raise RuntimeError("no H3 DiT block linears were selected for FP8 W8A8")

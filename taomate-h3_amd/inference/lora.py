@@ -17,6 +17,8 @@ Checkpoint loading (lora_checkpoint.py:61-150) is outside this package.
 
 from __future__ import annotations
 
+from collections.abc import Iterator
+from contextlib import contextmanager
 from typing import Any, Mapping
 
 import torch
@@ -71,8 +73,14 @@ def fused_quantized_lora_linear(base: Any, inputs: torch.Tensor, lora_a: torch.T
 
 class H3InferenceParallelLinearLoRA(torch.nn.Module):
     """LoRA wrapper of a column- or row-parallel base linear
-    (H3/inference/lora_checkpoint.py:172-205).  With one rank a row-parallel
-    base needs no reduction, so both kinds share the single-rank formula."""
+    (H3/inference/lora_checkpoint.py:172-205; FL/inference/lora_checkpoint.py:440-489).
+
+    ``adapter_enabled`` (FL) switches the side branch off: the wrapper then
+    returns the base output alone.  A row-parallel base split over several
+    tensor-parallel ranks needs the cross-rank reduction of its partial
+    output (with the LoRA partial added before it), which this single-GPU
+    build does not perform: such a call raises instead of returning a
+    partial sum."""
 
     def __init__(self, base: Any, *, kind: str, a: torch.Tensor, b: torch.Tensor, scale: float) -> None:
         super().__init__()
@@ -81,6 +89,7 @@ class H3InferenceParallelLinearLoRA(torch.nn.Module):
         self.base = base
         self.kind = kind
         self.scale = float(scale)
+        self.adapter_enabled = True
         self.fused_row_reduce_enabled = False
         self._taomate_h3_inference_lora = True
         self.register_buffer("lora_a", a, persistent=False)
@@ -89,12 +98,19 @@ class H3InferenceParallelLinearLoRA(torch.nn.Module):
     def forward(self, inputs: torch.Tensor) -> torch.Tensor:
         from .fused_kernels import as_dense
 
+        if not self.adapter_enabled:
+            return self.base(inputs)
+        if self.kind == "row" and int(getattr(self.base, "tp_size", 1)) > 1:
+            from ..distributed.linear import _cross_rank
+
+            raise _cross_rank("reducing a row-parallel LoRA output")
         inputs = as_dense(inputs)  # the LoRA branch needs the bf16 rows
         if _fusable(self.base, self.lora_a, self.lora_b):
             return fused_quantized_lora_linear(self.base, inputs, self.lora_a, self.lora_b, self.scale)
         output = self.base(inputs)
         compute_dtype = output.dtype
-        update = F.linear(F.linear(inputs.to(compute_dtype), self.lora_a), self.lora_b)
+        update = F.linear(F.linear(inputs.to(compute_dtype), self.lora_a.to(compute_dtype)),
+                          self.lora_b.to(compute_dtype))
         if tuple(update.shape) != tuple(output.shape):
             raise H3LoRACheckpointError("H3 inference LoRA output shape differs")
         return output + update * self.scale
@@ -127,7 +143,74 @@ def enable_h3_fused_lora_row_reduce_(transformer: Any) -> Mapping[str, Any]:
     return {"row_parallel_module_count": len(rows), "tp_all_reduce_calls_saved_per_forward": len(rows)}
 
 
+def _adapters(transformer: Any) -> list[tuple[str, Any]]:
+    return [(name, module) for name, module in transformer.named_modules()
+            if getattr(module, "_taomate_h3_inference_lora", False)]
+
+
+def merge_h3_lora_weights_(transformer: Any) -> Mapping[str, Any]:
+    """Fold each loaded adapter into its frozen base weight (FL/inference/lora_checkpoint.py:642-706):
+    W' = round_to_base_dtype(fp32(W) + scale * fp32(B) @ fp32(A)), once.  The
+    adapter is then switched off and its buffers released.  Quantized (W8)
+    bases cannot be merged (FL forbids the merge with W8A8,
+    FL/inference/acceleration.py:103-104)."""
+    adapters = _adapters(transformer)
+    if not adapters:
+        raise H3LoRACheckpointError("LoRA weight merge requires a loaded inference LoRA adapter")
+    merged_numel = released = 0
+    for name, module in adapters:
+        if not bool(module.adapter_enabled):
+            raise H3LoRACheckpointError(f"H3 inference LoRA target is already disabled: {name}")
+        weight = module.base.weight.detach()
+        if weight.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise H3LoRACheckpointError(f"H3 inference LoRA base weight cannot be merged: {name}")
+        if int(module.lora_a.shape[1]) != int(weight.shape[1]) or int(module.lora_b.shape[0]) != int(weight.shape[0]):
+            raise H3LoRACheckpointError(f"H3 inference LoRA local merge shape differs: {name}")
+        delta = module.lora_b.float() @ module.lora_a.float()
+        merged = (weight.float() + delta * float(module.scale)).to(weight.dtype)
+        module.base.weight = torch.nn.Parameter(merged, requires_grad=False)
+        merged_numel += int(merged.numel())
+        released += int(module.lora_a.numel() + module.lora_b.numel())
+        module.adapter_enabled = False
+        module._taomate_h3_lora_merged = True
+        del module.lora_a
+        del module.lora_b
+    return {
+        "schema": "digitalhuman_h3.inference.lora_weight_merge.v1",
+        "arithmetic": "fp32_delta_and_accumulate_then_round_to_base_dtype",
+        "target_count": len(adapters),
+        "merged_weight_numel": merged_numel,
+        "released_adapter_numel": released,
+        "online_lora_gemms_removed_per_forward": 2 * len(adapters),
+        "reversible": False,
+    }
+
+
+@contextmanager
+def h3_base_model_inference(transformer: Any) -> Iterator[None]:
+    """Run the base model with every adapter switched off, without consuming
+    FP8 activation-calibration samples (FL/inference/lora_checkpoint.py:709-739)."""
+    from ..distributed.linear import suspend_fp8_activation_calibration
+
+    modules = [module for _, module in _adapters(transformer)]
+    if not modules:
+        raise H3LoRACheckpointError("Base audio teacher requires an inference LoRA checkpoint")
+    if any(getattr(module, "_taomate_h3_lora_merged", False) for module in modules):
+        raise H3LoRACheckpointError("Base audio teacher cannot bypass an already merged LoRA weight")
+    previous = [bool(module.adapter_enabled) for module in modules]
+    for module in modules:
+        module.adapter_enabled = False
+    try:
+        with suspend_fp8_activation_calibration():
+            yield
+    finally:
+        for module, enabled in zip(modules, previous):
+            module.adapter_enabled = enabled
+
+
 __all__ = [
+    "h3_base_model_inference",
+    "merge_h3_lora_weights_",
     "FUSED_MAX_RANK",
     "H3InferenceParallelLinearLoRA",
     "H3LoRACheckpointError",

@@ -18,8 +18,9 @@ Module state keeps the reference's names, shapes and byte counts:
 (non-persistent), the stream-load flags and the optional workspace views.
 When N % 16 == 0 and K % 128 == 0 (every H3 projection) the codes in
 ``weight`` are stored in the GEMMs' tiled layout (16-row x 128-byte MFMA
-fragment tiles, include/taomate_h3_amd.h) and the parameter carries
-``_h3q_tiled = True``; otherwise they are row-major.  The tiled writer
+fragment tiles, include/taomate_h3_amd.h), recorded against the parameter's
+storage (``ops.is_tiled`` holds for the parameter and every view of it, such
+as ``weight.t()``); otherwise they are row-major.  The tiled writer
 quantizes straight into that layout, row chunk by row chunk.
 """
 
@@ -266,8 +267,6 @@ def cutlass_w8a8_linear(inputs: torch.Tensor, weight: torch.Tensor, weight_scale
     if workspace is not None:
         if weight_t is None:
             weight_t = weight.t()
-            if ops.is_tiled(weight):
-                ops.mark_tiled(weight_t)
         output = workspace.linear(flattened, weight_t, weight_scale.t() if weight_scale_t is None else weight_scale_t)
         return output.reshape(shape)
     if ops.is_tiled(weight):
@@ -353,8 +352,6 @@ def enable_h3_cutlass_w8a8_workspace_(transformer: Any) -> dict[str, Any]:
     for module in selected:
         module._cutlass_w8a8_workspace = workspace
         module._cutlass_w8a8_weight_t = module.weight.t()
-        if ops.is_tiled(module.weight):
-            ops.mark_tiled(module._cutlass_w8a8_weight_t)
         module._cutlass_w8a8_weight_scale_t = module._cutlass_w8a8_weight_scale.t()
     return {
         "linear_count": len(selected),

@@ -9,6 +9,7 @@ current HIP stream of the input's device.  Output tensors may be supplied
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 
@@ -168,14 +169,50 @@ def can_tile(rows: int, cols: int) -> bool:
     return rows > 0 and rows % 16 == 0 and cols > 0 and cols % 128 == 0
 
 
+# Storages that hold codes in the tiled layout.  The layout is a property of
+# the bytes, so it is recorded against the storage (its device address and
+# size): every view of a marked parameter -- ``weight.t()``, ``.data``,
+# ``.detach()``, slices -- resolves to the same entry, while a copy
+# (``.clone()``, ``.to()``, a new allocation at a reused address of another
+# size) does not.  An entry lives as long as the tensor that was marked.
+_TILED_STORAGES: dict[tuple[str, int, int], int] = {}
+
+
+def _storage_key(t: torch.Tensor) -> tuple[str, int, int]:
+    st = t.untyped_storage()
+    return (str(t.device), int(st.data_ptr()), int(st.nbytes()))
+
+
+def _unmark(key: tuple[str, int, int]) -> None:
+    count = _TILED_STORAGES.get(key, 0) - 1
+    if count > 0:
+        _TILED_STORAGES[key] = count
+    else:
+        _TILED_STORAGES.pop(key, None)
+
+
 def is_tiled(t: torch.Tensor | None) -> bool:
-    """True for a code tensor (or a view object) marked as holding the tiled layout."""
-    return bool(getattr(t, "_h3q_tiled", False))
+    """True when ``t`` (or any view of the same storage) holds tiled codes."""
+    if t is None or not isinstance(t, torch.Tensor) or t.device.type == "meta":
+        return False
+    return _storage_key(t) in _TILED_STORAGES
 
 
 def mark_tiled(t: torch.Tensor) -> torch.Tensor:
-    t._h3q_tiled = True
+    """Record that the storage of the code tensor ``t`` holds the tiled layout
+    (``t`` must cover its whole storage, as a freshly allocated weight does)."""
+    if t.data_ptr() != t.untyped_storage().data_ptr() or t.numel() * t.element_size() != t.untyped_storage().nbytes():
+        raise ValueError("mark_tiled: the tensor must cover its whole storage")
+    key = _storage_key(t)
+    _TILED_STORAGES[key] = _TILED_STORAGES.get(key, 0) + 1
+    weakref.finalize(t, _unmark, key)
     return t
+
+
+def check_layout(name: str, t: torch.Tensor, tiled: bool) -> None:
+    """Raise when a row-major call is made on a storage marked tiled."""
+    if not tiled and is_tiled(t):
+        raise ValueError(f"{name}: the operand's storage holds tiled codes; pass it with the tiled layout")
 
 
 def quant_activations_for(x: torch.Tensor, fmt: int, rounding: int, weight: torch.Tensor, *,
@@ -378,6 +415,8 @@ def scaled_mm(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor, b_scale: 
                              + (" (tiled operands are contiguous, rows rounded up to 16)" if tiled else ""))
     if b.shape[1] != k:
         raise ValueError(f"scaled_mm: inner dimensions differ ({k} vs {b.shape[1]})")
+    check_layout("scaled_mm a", a, a_tiled)
+    check_layout("scaled_mm b", b, b_tiled)
     ak = _scale_kind("scaled_mm a_scale", a_scale, m)
     bk = _scale_kind("scaled_mm b_scale", b_scale, n)
     if bias is not None:

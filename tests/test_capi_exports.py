@@ -54,13 +54,30 @@ def test_version_and_error_without_gpu():
     rc = lib.h3q_scaled_mm(0, None, 16, 0, None, 1, None, 16, 0, None, 1, None, None, 0, None, 0, 0, 1.0, None, 8,
                            4, 8, 24, None)
     assert rc == 1 and b"multiple of 16" in lib.h3q_last_error()
-    # tiled operands: k must be a multiple of 128; tiled activations only for m <= 128 without LoRA
+    # tiled operands: k must be a multiple of 128; tiled activations above 128
+    # rows need the four-wave GEMM's shapes (k >= 256, 8-column stores)
     rc = lib.h3q_scaled_mm(0, None, 0, 0, None, 1, None, 0, 1, None, 1, None, None, 0, None, 0, 0, 1.0, None, 8,
                            4, 8, 64, None)
     assert rc == 1 and b"multiple of 128" in lib.h3q_last_error()
     rc = lib.h3q_scaled_mm(0, None, 0, 1, None, 1, None, 0, 1, None, 1, None, None, 0, None, 0, 0, 1.0, None, 8,
                            256, 8, 128, None)
     assert rc == 2 and b"tiled activations" in lib.h3q_last_error()
+    rc = lib.h3q_scaled_mm(0, None, 0, 1, None, 1, None, 0, 1, None, 1, None, None, 0, None, 0, 0, 1.0, None, 12,
+                           256, 12, 256, None)
+    assert rc == 2 and b"tiled activations" in lib.h3q_last_error()
+    # tiled activations take no LoRA epilogue
+    p = ctypes.c_void_p(256)
+    rc = lib.h3q_scaled_mm(0, None, 0, 1, None, 1, None, 0, 1, None, 1, None, p, 128, p, 128, 128, 1.0, None, 8,
+                           256, 8, 256, None)
+    assert rc == 2 and b"LoRA" in lib.h3q_last_error()
+    # 256 rows of a tiled operand must sit below a 32-bit offset: 256 * k < 2^31
+    rc = lib.h3q_scaled_mm(0, None, 0, 1, None, 1, None, 0, 1, None, 1, None, None, 0, None, 0, 0, 1.0, None,
+                           8, 4, 8, 1 << 23, None)
+    assert rc == 2 and b"256 * k" in lib.h3q_last_error()
+    # LoRA row strides above 8 MiB are refused
+    rc = lib.h3q_scaled_mm(0, None, 128, 0, None, 1, None, 128, 0, None, 1, None, p, 1 << 22, p, 128, 128, 1.0,
+                           None, 8, 4, 8, 128, None)
+    assert rc == 2 and b"LoRA row stride" in lib.h3q_last_error()
     rc = lib.h3q_scaled_mm(0, None, 128, 5, None, 1, None, 128, 0, None, 1, None, None, 0, None, 0, 0, 1.0, None,
                            8, 4, 8, 128, None)
     assert rc == 1 and b"unknown operand layout" in lib.h3q_last_error()

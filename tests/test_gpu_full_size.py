@@ -1,0 +1,208 @@
+"""The BASELINE configurations at their own sizes, on the kernels the bench times.
+
+Every GEMM here runs at full size on the GPU; the CPU oracle checks a
+stratified set of output rows: at least one row of every 256-row tile-row,
+plus the tile boundaries (rows 255 and 256) and the last row, across all N
+columns.  With more tiles than workgroups, each workgroup walks several
+tiles, so these rows also cover the hand-over from one tile to the next.
+
+* int8: int32 accumulators and bf16 outputs bit-exact against the oracle's
+  s_a * (s_w * float(acc)) epilogue.
+* e4m3: against the oracle's model of the FP8 matrix instruction, within the
+  per-element bound of ``_assert_fp8_close`` (almost all outputs bit-identical).
+* LoRA (c3): against the reference's three rounding points
+  (H3/inference/lora_checkpoint.py:196-205), within 4 bf16 ulps of the
+  output and 2^-7 relative error.
+
+References: H3/inference/w8a8.py:178-186 (per-token int8 + CUTLASS GEMM),
+FL/distributed/linear.py:92-100 (FP8 GEMM), H3/inference/lora_checkpoint.py:196-205.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _util import activations, bf16_ulp, bits16, bits8, weights
+from test_gpu_gemm import _assert_fp8_close
+
+pytestmark = pytest.mark.gpu
+
+
+def stratified_rows(m: int, seed: int = 0, per_tile: int = 1) -> np.ndarray:
+    """One (or more) seeded row of every 256-row tile-row, plus rows 0, 255,
+    256 and m - 1."""
+    rng = np.random.default_rng(seed)
+    rows = {0, min(255, m - 1), min(256, m - 1), m - 1}
+    for t in range((m + 255) // 256):
+        lo, hi = 256 * t, min(256 * t + 256, m)
+        rows.update(int(r) for r in rng.integers(lo, hi, size=per_tile))
+    return np.array(sorted(rows))
+
+
+def _bias(n: int, seed: int) -> torch.Tensor:
+    return (torch.randn(n, generator=torch.Generator().manual_seed(seed)) * 0.01).to(torch.bfloat16)
+
+
+def _quant_weights(ops, w, device, fmt):
+    f = ops.FMT_E4M3FN if fmt == "e4m3" else ops.FMT_INT8
+    return ops.quant_rows_tiled(w.to(device), f, ops.ROUND_DIV)
+
+
+@pytest.mark.parametrize("a_tiled", [False, True])
+def test_c2_qkv_tiled_weights_stratified(ops, oracle, device, a_tiled):
+    """c2 (M=8192, K=5120, N=15360, e4m3, bias): the bench's instance (tiled
+    weights), with row-major and with tiled activations; 1920 tiles over the
+    persistent grid, so every workgroup runs several tiles."""
+    m, k, n = 8192, 5120, 15360
+    print(f"c2 tiled weights a_tiled={a_tiled}", flush=True)
+    x = activations(m, k, seed=0, outlier_channels=k // 100, outlier_scale=15.0)
+    w = weights(n, k, seed=1)
+    bias = _bias(n, 2)
+    qw, sw = _quant_weights(ops, w, device, "e4m3")
+    xg = x.to(device)
+    if a_tiled:
+        qa, sa = ops.quant_rows_tiled(xg, ops.FMT_E4M3FN, ops.ROUND_DIV)
+    else:
+        qa, sa = ops.quant_rows(xg, ops.FMT_E4M3FN)
+    out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), bias=bias.to(device), a_tiled=a_tiled,
+                        b_tiled=True, m=m, n=n)
+    torch.cuda.synchronize()
+    rows = stratified_rows(m)
+    rqa, rsa = oracle.quant_rows(bits16(x[torch.from_numpy(rows)]), "e4m3")
+    rqw, rsw = oracle.quant_rows(bits16(w), "e4m3")
+    np.testing.assert_array_equal(sw.cpu().numpy().ravel(), rsw)
+    _assert_fp8_close(oracle, bits16(out)[rows], rqa, rsa, rqw, rsw, bits16(bias))
+
+
+def test_c2_row_major_and_tiled_layouts_agree(ops, device):
+    """The four operand-layout combinations of the c2 GEMM give the same bits."""
+    m, k, n = 8192, 5120, 15360
+    x = activations(m, k, seed=3, outlier_channels=k // 100, outlier_scale=15.0).to(device)
+    w = weights(n, k, seed=4).to(device)
+    bias = _bias(n, 5).to(device)
+    qa, sa = ops.quant_rows(x, ops.FMT_E4M3FN)
+    qat, _ = ops.quant_rows_tiled(x, ops.FMT_E4M3FN, ops.ROUND_DIV)
+    qw, sw = ops.quant_rows(w, ops.FMT_E4M3FN)
+    qwt, _ = ops.quant_rows_tiled(w, ops.FMT_E4M3FN, ops.ROUND_DIV)
+    outs = []
+    for a, at in ((qa, False), (qat, True)):
+        for b, bt in ((qw, False), (qwt, True)):
+            outs.append(ops.scaled_mm(a, b, sa.reshape(-1), sw.reshape(-1), bias=bias, a_tiled=at, b_tiled=bt,
+                                      m=m, n=n))
+    torch.cuda.synchronize()
+    ref = bits16(outs[0])
+    for o in outs[1:]:
+        np.testing.assert_array_equal(bits16(o), ref)
+
+
+@pytest.mark.parametrize("which", ["up", "down"])
+def test_c3_ffn_lora_stratified(ops, oracle, device, which):
+    """c3 (768p FFN, M=24576): up N=13824 K=5120 and down N=5120 K=13824,
+    e4m3 tiled weights, rank-128 bf16 LoRA with alpha=128 (scale 1.0) in the
+    GEMM epilogue."""
+    m = 24576
+    n, k = (13824, 5120) if which == "up" else (5120, 13824)
+    rank = 128
+    print(f"c3 {which}: {m}x{n}x{k} LoRA rank {rank}", flush=True)
+    x = activations(m, k, seed=7, outlier_channels=0)
+    w = weights(n, k, seed=8)
+    gen = torch.Generator().manual_seed(9)
+    la = (torch.randn(rank, k, generator=gen) * 0.01).to(torch.bfloat16)
+    lb = (torch.randn(n, rank, generator=gen) * 0.01).to(torch.bfloat16)
+    xg = x.to(device)
+    qw, sw = _quant_weights(ops, w, device, "e4m3")
+    qa, sa = ops.quant_rows(xg, ops.FMT_E4M3FN)
+    t = ops.lora_down(xg, la.to(device))
+    out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), lora_t=t, lora_b=lb.to(device), lora_scale=1.0,
+                        b_tiled=True, n=n)
+    torch.cuda.synchronize()
+    rows = stratified_rows(m, seed=1)
+    xr = bits16(x[torch.from_numpy(rows)])
+    rqa, rsa = oracle.quant_rows(xr, "e4m3")
+    rqw, rsw = oracle.quant_rows(bits16(w), "e4m3")
+    base = oracle.epilogue(oracle.gemm_e4m3_mfma(rqa, rqw)[0], rsa, rsw)
+    ref = oracle.bf16_to_f32(oracle.lora_reference(xr, bits16(la), bits16(lb), 1.0, base)).astype(np.float64)
+    got = oracle.bf16_to_f32(bits16(out)[rows]).astype(np.float64)
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert rel <= 2.0 ** -7, rel
+    err = np.abs(got - ref)
+    assert np.all(err <= 4 * bf16_ulp(np.maximum(np.abs(ref), np.abs(got))) + 1e-30), err.max()
+
+
+def test_c5_int8_full_size_bit_exact(ops, oracle, device):
+    """c5 (1080p, M=40960, K=N=5120, int8 with Student-t outlier channels):
+    per-token vLLM-form activation codes, per-channel weight codes (tiled),
+    bf16 outputs bit-exact on the stratified rows; int32 accumulators
+    bit-exact on the same rows."""
+    m, k, n = 40960, 5120, 5120
+    print("c5 int8 full size", flush=True)
+    x = activations(m, k, seed=11, outlier_channels=k // 100, student_t=True)
+    w = weights(n, k, seed=12)
+    xg = x.to(device)
+    qw, sw = _quant_weights(ops, w, device, "int8")
+    qa, sa = ops.quant_rows(xg, ops.FMT_INT8, ops.ROUND_RCP_MUL)
+    out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), b_tiled=True, n=n)
+    torch.cuda.synchronize()
+    rows = stratified_rows(m, seed=2)
+    rqa, rsa = oracle.quant_rows(bits16(x[torch.from_numpy(rows)]), "int8", "rcp")
+    np.testing.assert_array_equal(bits8(qa)[rows], rqa.view(np.uint8))
+    rqw, rsw = oracle.quant_rows(bits16(w), "int8", "div")
+    acc = oracle.gemm_i8_i32(rqa, rqw)
+    np.testing.assert_array_equal(bits16(out)[rows], oracle.epilogue(acc, rsa, rsw))
+    # raw accumulators of the same rows through the integer entry point
+    qw_rows, _ = ops.quant_rows(w.to(device), ops.FMT_INT8, ops.ROUND_DIV)
+    acc_gpu = ops.gemm_i8_i32(qa[torch.from_numpy(rows).to(device)].contiguous(), qw_rows)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(acc_gpu.cpu().numpy(), acc)
+
+
+@pytest.mark.parametrize("fmt", ["int8", "e4m3"])
+@pytest.mark.parametrize("per_tensor", [False, True])
+def test_more_tiles_than_workgroups(ops, oracle, device, fmt, per_tensor):
+    """m=4608, n=4096, k=1024 with tiled weights and bias: 288 output tiles,
+    more than the persistent grid, so 32 workgroups run a second tile.
+    int8: every row bit-exact.  e4m3: whole tile-rows 0, 8 and 17 and the
+    boundaries against the instruction model.  Per-row and per-tensor scales."""
+    m, n, k = 4608, 4096, 1024
+    f = ops.FMT_E4M3FN if fmt == "e4m3" else ops.FMT_INT8
+    ar = ops.ROUND_DIV if fmt == "e4m3" else ops.ROUND_RCP_MUL
+    x = activations(m, k, seed=13, outlier_channels=10, outlier_scale=15.0)
+    w = weights(n, k, seed=14)
+    bias = _bias(n, 15)
+    qw, sw = _quant_weights(ops, w, device, fmt)
+    qa, sa = ops.quant_rows(x.to(device), f, ar)
+    if per_tensor:
+        sa = sa.reshape(-1)[:1].clone()
+        sw = sw.reshape(-1)[:1].clone()
+    out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), bias=bias.to(device), b_tiled=True, n=n)
+    torch.cuda.synchronize()
+    rqa, rsa = oracle.quant_rows(bits16(x), fmt, "div" if fmt == "e4m3" else "rcp")
+    rqw, rsw = oracle.quant_rows(bits16(w), fmt, "div")
+    if per_tensor:
+        rsa, rsw = rsa[:1], rsw[:1]
+    if fmt == "int8":
+        ref = oracle.epilogue(oracle.gemm_i8_i32(rqa, rqw), rsa, rsw, bits16(bias))
+        np.testing.assert_array_equal(bits16(out), ref)
+    else:
+        rows = np.unique(np.concatenate([np.arange(0, 256), np.arange(2048, 2304), np.arange(4352, 4608),
+                                         [255, 256, 511, 512, 4607]]))
+        _assert_fp8_close(oracle, bits16(out)[rows], rqa[rows], rsa if per_tensor else rsa[rows], rqw, rsw,
+                          bits16(bias))
+
+
+def test_ragged_large_m_tiled_activations(ops, oracle, device):
+    """A ragged M (not a multiple of 16 or 256) with tiled activations and
+    tiled weights through the four-wave GEMM, int8: every output bit-exact."""
+    m, n, k = 1000, 3000, 1024
+    x = activations(m, k, seed=17, outlier_channels=5)
+    w = weights(n - 8, k, seed=18)            # n = 2992: a partial last tile column
+    n = n - 8
+    qw, sw = _quant_weights(ops, w, device, "int8")
+    qa, sa = ops.quant_rows_tiled(x.to(device), ops.FMT_INT8, ops.ROUND_RCP_MUL)
+    out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), a_tiled=True, b_tiled=True, m=m, n=n)
+    torch.cuda.synchronize()
+    rqa, rsa = oracle.quant_rows(bits16(x), "int8", "rcp")
+    rqw, rsw = oracle.quant_rows(bits16(w), "int8", "div")
+    np.testing.assert_array_equal(bits16(out), oracle.epilogue(oracle.gemm_i8_i32(rqa, rqw), rsa, rsw))

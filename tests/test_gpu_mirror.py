@@ -15,6 +15,7 @@ import torch
 
 from _util import activations, bits8, bits16, to_tiled, weights
 from test_gpu_gemm import _assert_fp8_close
+import taomate_h3_amd.ops as ops_mod
 
 pytestmark = pytest.mark.gpu
 
@@ -77,7 +78,7 @@ def test_stream_load_chunks_equal_whole_matrix(oracle, device, rows, k, limit):
     torch.cuda.synchronize()
     rq, rs = oracle.quant_rows(bits16(src), "int8", "div")
     tiled = rows % 16 == 0 and k % 128 == 0
-    assert getattr(m.weight, "_h3q_tiled", False) == tiled
+    assert ops_mod.is_tiled(m.weight) == tiled
     expect = to_tiled(rq.view(np.uint8)) if tiled else rq.view(np.uint8)
     np.testing.assert_array_equal(bits8(m.weight), expect)
     np.testing.assert_array_equal(m._cutlass_w8a8_weight_scale.cpu().numpy().ravel(), rs)
@@ -146,7 +147,7 @@ def test_model_level_int8_flow(oracle, device):
     assert receipt["linear_count"] == 4 and receipt["post_load_conversion_linear_count"] == 0
     assert receipt["quantized_weight_bytes"] * 2 == receipt["source_weight_bytes"]
     assert w8a8.enable_h3_cutlass_w8a8_workspace_(model)["linear_count"] == 4
-    assert all(getattr(model.get_submodule(n).weight, "_h3q_tiled", False) for n in names["quantized_linear_names"])
+    assert all(ops_mod.is_tiled(model.get_submodule(n).weight) for n in names["quantized_linear_names"])
     for tokens in (2 * 96, 2 * 40, 7):   # large GEMM, then the weight-streaming GEMM (tiled activations)
         x = activations(tokens, 256, seed=12 + tokens, outlier_channels=2)
         for name in ("blocks.2.attn.qkv_proj", "blocks.3.mlp.fc1"):
@@ -197,7 +198,7 @@ def test_fp8_w8a8_module_dispatch(oracle, device):
     fc2 = model.get_submodule("blocks.2.mlp.fc2")
     assert fc2.weight.dtype == torch.bfloat16
     fc1 = model.get_submodule("blocks.2.mlp.fc1")
-    assert getattr(fc1.weight, "_h3q_tiled", False)
+    assert ops_mod.is_tiled(fc1.weight)
     rqw, rsw = oracle.quant_rows(bits16(originals["blocks.2.mlp.fc1"]), "e4m3")
     np.testing.assert_array_equal(bits8(fc1.weight), to_tiled(rqw))
     for tokens in (150, 48):   # large GEMM, then the weight-streaming GEMM

@@ -173,3 +173,26 @@ def test_tiled_quantizer_matches_permuted_oracle(ops, oracle, device, fmt, round
     rq, rs = oracle.quant_rows(bits16(w), fmt, rounding)
     np.testing.assert_array_equal(bits8(codes), to_tiled(rq.view(np.uint8)))
     np.testing.assert_array_equal(scales.cpu().numpy().ravel(), rs)
+
+
+def test_int8_rcp_known_answers(ops, device):
+    """The vLLM-form kernel (h3q_quant_rows INT8 + RCP_MUL) against closed-form
+    known answers evaluated in exact rational arithmetic (tests/_exact32.py):
+    the half-integer ties where the reciprocal-multiply and division forms
+    disagree, +-amax -> +-127, and a zero row."""
+    import _exact32 as E
+
+    cases = E.separating_cases()
+    k = 64
+    rows = np.zeros((len(cases) + 1, k), dtype=np.float32)
+    for r, (x, amax, _, _) in enumerate(cases):
+        rows[r, 0], rows[r, 1], rows[r, 2], rows[r, 3] = amax, x, -x, -amax
+    x = torch.from_numpy(rows).to(torch.bfloat16)
+    q, s = _run_rows(ops, x.to(device), "int8", "rcp")
+    q = q.view(np.int8)
+    for r, (xv, amax, q_rcp, q_div) in enumerate(cases):
+        assert (q[r, 1], q[r, 2]) == (q_rcp, -q_rcp), (xv, amax, q[r, 1], q_rcp)
+        assert q[r, 1] != q_div
+        assert (q[r, 0], q[r, 3]) == (127, -127)
+        assert s[r] == np.float32(float(E.int8_scale(amax)))
+    assert s[-1] == 0.0 and not q[-1].any()

@@ -299,6 +299,65 @@ def test_vllm_int8_rcp_invariants(oracle):
     assert np.all(err <= s[:, None] * 0.5 + np.abs(xf) * 2.0 ** -22 + 1e-30)
 
 
+def _rcp_kat_rows(cases, k=64):
+    """One row per (x, amax) case: [amax, x, -x, -amax, 0, ...] (bf16)."""
+    rows = np.zeros((len(cases), k), dtype=np.float32)
+    for r, (x, amax, _, _) in enumerate(cases):
+        rows[r, 0], rows[r, 1], rows[r, 2], rows[r, 3] = amax, x, -x, -amax
+    return torch.from_numpy(rows).to(torch.bfloat16)
+
+
+def test_vllm_int8_rcp_known_answers(oracle):
+    """vLLM's per-token int8 quantizer (dynamic_scaled_int8_quant, called at
+    H3/inference/w8a8.py:178; third-party, absent here) computes
+    q = sat8(rne(fl(x * fl(127 / amax)))) and stores fl(amax / 127).  The
+    known answers are evaluated step by step in exact rational arithmetic
+    (tests/_exact32.py), independently of numpy and torch, on the inputs where
+    that form and the division form rne(fl(x / fl(amax / 127))) disagree:
+    the half-integer ties x = amax / 2.  The oracle must return the
+    reciprocal-multiply codes, and on every case the division form must
+    disagree with it, so a division-form oracle fails this test."""
+    import _exact32 as E
+
+    cases = E.separating_cases()
+    assert len(cases) >= 20
+    assert any(c[2] > c[3] for c in cases) and any(c[2] < c[3] for c in cases)
+    x = _rcp_kat_rows(cases)
+    q, s = oracle.quant_rows(bits16(x), "int8", "rcp")
+    for r, (xv, amax, q_rcp, q_div) in enumerate(cases):
+        assert q[r, 1] == q_rcp and q[r, 2] == -q_rcp, (xv, amax, q[r, 1], q_rcp)
+        assert q[r, 1] != q_div                      # the division form is excluded
+        assert q[r, 0] == 127 and q[r, 3] == -127    # saturation never reaches -128
+        assert not q[r, 4:].any()
+        assert s[r] == np.float32(float(E.int8_scale(amax)))
+
+
+def test_vllm_int8_rcp_random_known_answers(oracle):
+    """Random bf16 rows against the exact closed form element by element, plus
+    the zero row (scale 0, all codes 0) and a row whose largest magnitude is
+    negative (it maps to -127, never -128)."""
+    import _exact32 as E
+
+    rng = np.random.default_rng(11)
+    vals = np.asarray(E.bf16_values(0x3A00, 0x4380, 7), dtype=np.float32)
+    rows = []
+    for _ in range(24):
+        rows.append(rng.choice(vals, 48) * rng.choice([-1.0, 1.0], 48))
+    rows = np.stack(rows).astype(np.float32)
+    rows[5] = 0.0
+    rows[6, 0] = -np.abs(rows[6]).max() * 2
+    x = torch.from_numpy(rows).to(torch.bfloat16)
+    xf = x.float().numpy()
+    q, s = oracle.quant_rows(bits16(x), "int8", "rcp")
+    for r in range(xf.shape[0]):
+        amax = float(np.abs(xf[r]).max())
+        assert s[r] == np.float32(float(E.int8_scale(amax)))
+        expect = [E.int8_rcp_mul(float(v), amax) for v in xf[r]]
+        np.testing.assert_array_equal(q[r].astype(np.int64), expect)
+    assert s[5] == 0.0 and not q[5].any()
+    assert q[6, 0] == -127
+
+
 # ---------------------------------------------------------------------- GEMMs
 
 def test_int8_gemm_matches_torch_int_mm_and_brute_force(oracle):

@@ -19,6 +19,7 @@ import torch
 from safetensors.torch import save_file
 
 from _util import bits16, to_tiled
+import taomate_h3_amd.ops as ops_mod
 
 HEADS, HEAD_DIM, HIDDEN, FFN = 4, 32, 256, 512
 
@@ -210,7 +211,7 @@ def test_streamed_w8a8_slots_match_the_oracle(tmp_path, oracle, device):
     for name in slots:
         module = model.get_submodule(name)
         rq, rs = oracle.quant_rows(bits16(expect[name + ".weight"]), "int8", "div")
-        assert getattr(module.weight, "_h3q_tiled", False)
+        assert ops_mod.is_tiled(module.weight)
         np.testing.assert_array_equal(module.weight.detach().view(torch.uint8).cpu().numpy(),
                                       to_tiled(rq.view(np.uint8)))
         np.testing.assert_array_equal(module._cutlass_w8a8_weight_scale.cpu().numpy().ravel(), rs)
