@@ -1,8 +1,9 @@
-"""Linear layers and the quantized-linear dispatch (mirror of taomate_h3.distributed.linear)."""
+"""The quantized-linear dispatch of the parallel linear layers (mirror of taomate_h3.distributed.linear)."""
 
 from .linear import (  # noqa: F401
-    ColumnParallelLinear,
-    MergedColumnParallelLinear,
-    ParallelContext,
-    RowParallelLinear,
+    _linear,
+    _module_fp8_input_scale,
+    _module_linear,
+    suspend_fp8_activation_calibration,
+    use_fp8_activation_scale_policy,
 )

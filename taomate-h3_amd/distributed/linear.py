@@ -1,4 +1,4 @@
-"""Parallel linear layers and the quantized-linear dispatch.
+"""The quantized-linear dispatch of the parallel linear layers.
 
 Drop-in for the quantized-linear seam of H3/distributed/linear.py:15-191 and
 FL/distributed/linear.py:16-181:
@@ -13,20 +13,18 @@ FL/distributed/linear.py:16-181:
 * ``_module_fp8_input_scale`` and the two context managers keep FL's
   calibrated-scale protocol (FL/distributed/linear.py:16-47,104-128).
 
-This build runs on one GPU.  A ``ParallelContext`` may name any TP rank, so
-one rank's shard is sliced, loaded and run exactly as on a TP node (a
-column-parallel linear without output gather needs nothing from the other
-ranks); the steps that exchange data across ranks (the output gather of a
-column-parallel linear, the reduction of a row-parallel one) raise
-``NotImplementedError`` when the context has more than one rank.
+The parallel linear layers themselves (ColumnParallelLinear,
+MergedColumnParallelLinear, RowParallelLinear) stay the reference's: their
+forward calls ``_module_linear``, which this module replaces.  This build runs
+on one GPU; steps that exchange data across tensor-parallel ranks raise
+``NotImplementedError`` (``_cross_rank``).
 """
 
 from __future__ import annotations
 
-from collections.abc import Iterator, Sequence
+from collections.abc import Iterator
 from contextlib import contextmanager
 from contextvars import ContextVar
-from dataclasses import dataclass
 
 import torch
 import torch.nn as nn
@@ -35,28 +33,8 @@ import torch.nn.functional as F
 from .. import ops
 
 
-@dataclass(frozen=True)
-class ParallelContext:
-    """Tensor-parallel placement of this rank (H3/distributed/parallel.py:9-31;
-    the process groups are not part of this single-GPU build)."""
-
-    tp_world_size: int = 1
-    tp_rank: int = 0
-
-    def __post_init__(self) -> None:
-        if self.tp_world_size <= 0 or not 0 <= self.tp_rank < self.tp_world_size:
-            raise ValueError(f"invalid tp topology: world_size={self.tp_world_size}, rank={self.tp_rank}")
-
-
 def _cross_rank(what: str) -> NotImplementedError:
     return NotImplementedError(f"{what} across tensor-parallel ranks is not part of this single-GPU build")
-
-
-_DEFAULT_CONTEXT = ParallelContext()
-
-
-def current_parallel_context() -> ParallelContext:
-    return _DEFAULT_CONTEXT
 
 
 # ------------------------------------------------------------------ dispatch
@@ -203,128 +181,11 @@ def _module_fp8_input_scale(module: nn.Module, inputs: torch.Tensor) -> torch.Te
     return scale * margin
 
 
-# ------------------------------------------------------------ linear layers
-
-class ColumnParallelLinear(nn.Module):
-    """Output-column linear (H3/distributed/linear.py:36-88)."""
-
-    def __init__(self, input_size: int, output_size: int, *, bias: bool, gather_output: bool,
-                 dtype: torch.dtype, context: ParallelContext | None = None, weight_requires_grad: bool = True,
-                 device: torch.device | str | None = None) -> None:
-        super().__init__()
-        self.parallel_context = context or current_parallel_context()
-        self.input_size = int(input_size)
-        self.output_size = int(output_size)
-        self.tp_size = self.parallel_context.tp_world_size
-        self.tp_rank = self.parallel_context.tp_rank
-        self.gather_output = bool(gather_output)
-        if self.output_size % self.tp_size:
-            raise ValueError(f"column output {self.output_size} is not divisible by TP={self.tp_size}")
-        self.local_output_size = self.output_size // self.tp_size
-        self.weight = nn.Parameter(torch.empty(self.local_output_size, self.input_size, dtype=dtype, device=device),
-                                   requires_grad=weight_requires_grad)
-        self.bias = nn.Parameter(torch.empty(self.local_output_size, dtype=dtype, device=device)) if bias else None
-
-    def forward(self, inputs: torch.Tensor) -> torch.Tensor:
-        output = _module_linear(self, inputs, self.bias)
-        if self.gather_output and self.tp_size > 1:
-            raise _cross_rank("gathering the output")
-        return output
-
-    def full_weight_slice(self, value: torch.Tensor) -> torch.Tensor:
-        if tuple(value.shape) != (self.output_size, self.input_size):
-            raise ValueError("full column-parallel weight shape differs")
-        return value.narrow(0, self.tp_rank * self.local_output_size, self.local_output_size).contiguous()
-
-    def full_bias_slice(self, value: torch.Tensor) -> torch.Tensor:
-        if tuple(value.shape) != (self.output_size,):
-            raise ValueError("full column-parallel bias shape differs")
-        return value.narrow(0, self.tp_rank * self.local_output_size, self.local_output_size).contiguous()
-
-
-class MergedColumnParallelLinear(ColumnParallelLinear):
-    """Column sharding applied to fused logical projections (H3/distributed/linear.py:91-137)."""
-
-    def __init__(self, input_size: int, output_sizes: Sequence[int], *, bias: bool, gather_output: bool,
-                 dtype: torch.dtype, context: ParallelContext | None = None, weight_requires_grad: bool = True,
-                 device: torch.device | str | None = None) -> None:
-        self.output_sizes = tuple(int(v) for v in output_sizes)
-        if not self.output_sizes or any(v <= 0 for v in self.output_sizes):
-            raise ValueError("merged column output sizes must be positive")
-        active = context or current_parallel_context()
-        if any(v % active.tp_world_size for v in self.output_sizes):
-            raise ValueError("every merged output must be divisible by TP")
-        super().__init__(input_size, sum(self.output_sizes), bias=bias, gather_output=gather_output, dtype=dtype,
-                         context=active, weight_requires_grad=weight_requires_grad, device=device)
-        self.local_output_sizes = tuple(v // self.tp_size for v in self.output_sizes)
-
-    def _pieces(self, value: torch.Tensor) -> torch.Tensor:
-        pieces, offset = [], 0
-        for size, local in zip(self.output_sizes, self.local_output_sizes):
-            pieces.append(value.narrow(0, offset + self.tp_rank * local, local))
-            offset += size
-        return torch.cat(pieces, dim=0).contiguous()
-
-    def full_weight_slice(self, value: torch.Tensor) -> torch.Tensor:
-        if tuple(value.shape) != (self.output_size, self.input_size):
-            raise ValueError("full merged-column weight shape differs")
-        return self._pieces(value)
-
-    def full_bias_slice(self, value: torch.Tensor) -> torch.Tensor:
-        if tuple(value.shape) != (self.output_size,):
-            raise ValueError("full merged-column bias shape differs")
-        return self._pieces(value)
-
-
-class RowParallelLinear(nn.Module):
-    """Input-row linear (H3/distributed/linear.py:140-191).  With one rank the
-    partial output is the full output and the reduction is the identity."""
-
-    def __init__(self, input_size: int, output_size: int, *, bias: bool, dtype: torch.dtype,
-                 context: ParallelContext | None = None, input_is_parallel: bool = True,
-                 weight_requires_grad: bool = True, device: torch.device | str | None = None) -> None:
-        super().__init__()
-        self.parallel_context = context or current_parallel_context()
-        self.input_size = int(input_size)
-        self.output_size = int(output_size)
-        self.tp_size = self.parallel_context.tp_world_size
-        self.tp_rank = self.parallel_context.tp_rank
-        self.input_is_parallel = bool(input_is_parallel)
-        self.inference_inplace_reduce_enabled = False
-        if self.input_size % self.tp_size:
-            raise ValueError(f"row input {self.input_size} is not divisible by TP={self.tp_size}")
-        self.local_input_size = self.input_size // self.tp_size
-        self.weight = nn.Parameter(torch.empty(self.output_size, self.local_input_size, dtype=dtype, device=device),
-                                   requires_grad=weight_requires_grad)
-        self.bias = nn.Parameter(torch.empty(self.output_size, dtype=dtype, device=device)) if bias else None
-
-    def forward_local(self, inputs: torch.Tensor) -> torch.Tensor:
-        """This rank's partial output before reduction and bias."""
-        return _module_linear(self, inputs, None)
-
-    def reduce_local_output(self, value: torch.Tensor) -> torch.Tensor:
-        if self.tp_size > 1:
-            raise _cross_rank("reducing the output")
-        return value
-
-    def forward(self, inputs: torch.Tensor) -> torch.Tensor:
-        output = self.reduce_local_output(self.forward_local(inputs))
-        if self.bias is not None:
-            output = output + self.bias
-        return output
-
-    def full_weight_slice(self, value: torch.Tensor) -> torch.Tensor:
-        if tuple(value.shape) != (self.output_size, self.input_size):
-            raise ValueError("full row-parallel weight shape differs")
-        return value.narrow(1, self.tp_rank * self.local_input_size, self.local_input_size).contiguous()
-
-
 __all__ = [
-    "ColumnParallelLinear",
-    "MergedColumnParallelLinear",
-    "ParallelContext",
-    "RowParallelLinear",
-    "current_parallel_context",
+    "_cross_rank",
+    "_linear",
+    "_module_fp8_input_scale",
+    "_module_linear",
     "suspend_fp8_activation_calibration",
     "use_fp8_activation_scale_policy",
 ]

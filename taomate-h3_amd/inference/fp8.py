@@ -144,15 +144,21 @@ def quantize_aligned_linears_dynamic_fp8_(torch: Any, module: Any) -> dict[str, 
             "linear_count": len(names)}
 
 
-def _block_candidates(transformer: Any, suffixes: tuple[str, ...]) -> list[tuple[str, Any]]:
-    from ..distributed.linear import ColumnParallelLinear, RowParallelLinear
+def _is_parallel_linear(module: Any) -> bool:
+    """A tensor-parallel linear of the reference (column, merged-column or
+    row): a module with a 2-D weight and the ``input_size`` / ``output_size``
+    those classes carry (FL/distributed/linear.py:131-181)."""
+    weight = getattr(module, "weight", None)
+    return getattr(weight, "ndim", 0) == 2 and hasattr(module, "input_size") and hasattr(module, "output_size")
 
+
+def _block_candidates(transformer: Any, suffixes: tuple[str, ...]) -> list[tuple[str, Any]]:
     found = []
     for name, module in transformer.named_modules():
         if not name.startswith("blocks.") or not name.endswith(suffixes):
             continue
         base = getattr(module, "base", module)
-        if isinstance(base, (ColumnParallelLinear, RowParallelLinear)):
+        if _is_parallel_linear(base):
             found.append((name, base))
     return found
 

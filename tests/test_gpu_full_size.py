@@ -11,8 +11,9 @@ tiles, so these rows also cover the hand-over from one tile to the next.
 * e4m3: against the oracle's model of the FP8 matrix instruction, within the
   per-element bound of ``_assert_fp8_close`` (almost all outputs bit-identical).
 * LoRA (c3): against the reference's three rounding points
-  (H3/inference/lora_checkpoint.py:196-205), within 4 bf16 ulps of the
-  output and 2^-7 relative error.
+  (H3/inference/lora_checkpoint.py:196-205): per element within one bf16
+  ulp of each of the three rounded quantities plus the FP8 accumulator
+  bound, 99% within one ulp of the output, and 2^-7 relative error.
 
 References: H3/inference/w8a8.py:178-186 (per-token int8 + CUTLASS GEMM),
 FL/distributed/linear.py:92-100 (FP8 GEMM), H3/inference/lora_checkpoint.py:196-205.
@@ -120,15 +121,39 @@ def test_c3_ffn_lora_stratified(ops, oracle, device, which):
     torch.cuda.synchronize()
     rows = stratified_rows(m, seed=1)
     xr = bits16(x[torch.from_numpy(rows)])
+    # t = bf16(x @ A^T): the GPU's binary32 sum over K and the oracle's binary64
+    # one round to bf16 within one ulp of each other (plus the binary32 sum error).
+    t_exact = oracle.lora_down_reference(xr, bits16(la))
+    t_gpu = oracle.bf16_to_f32(bits16(t)[rows]).astype(np.float64)
+    t_abs = np.abs(oracle.bf16_to_f32(xr).astype(np.float64)) @ np.abs(oracle.bf16_to_f32(bits16(la))).T
+    assert np.all(np.abs(t_gpu - t_exact) <= bf16_ulp(np.abs(t_exact)) + k * 2.0 ** -24 * t_abs)
+    # The epilogue is then checked from the GPU's t, with the reference's
+    # rounding points (H3/inference/lora_checkpoint.py:196-205):
+    #   u = bf16(t @ B^T); out = bf16(base + bf16(u * 1.0)).
     rqa, rsa = oracle.quant_rows(xr, "e4m3")
     rqw, rsw = oracle.quant_rows(bits16(w), "e4m3")
-    base = oracle.epilogue(oracle.gemm_e4m3_mfma(rqa, rqw)[0], rsa, rsw)
-    ref = oracle.bf16_to_f32(oracle.lora_reference(xr, bits16(la), bits16(lb), 1.0, base)).astype(np.float64)
+    model, rbound = oracle.gemm_e4m3_mfma(rqa, rqw)
+    base_f = oracle.bf16_to_f32(oracle.epilogue(model, rsa, rsw)).astype(np.float64)
+    lbf = oracle.bf16_to_f32(bits16(lb)).astype(np.float64)
+    upd = oracle.bf16_to_f32(oracle.f32_to_bf16_fast((t_gpu @ lbf.T).astype(np.float32))).astype(np.float64)
+    ref = oracle.bf16_to_f32(oracle.f32_to_bf16_fast((base_f + upd).astype(np.float32))).astype(np.float64)
     got = oracle.bf16_to_f32(bits16(out)[rows]).astype(np.float64)
     rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
     assert rel <= 2.0 ** -7, rel
+    # The reference rounds the base output, the update and the sum to bf16
+    # (three roundings); the fused epilogue rounds the binary32 sum once.  Per
+    # element the two differ by at most an ulp of each rounded quantity, plus
+    # what separates the GPU's accumulators from the oracle's models: the FP8
+    # instruction's binary32 combination rounding (rbound, times the two
+    # scales), the epilogue's scale products (2^-22 relative) and the binary32
+    # sum over the rank (rank * 2^-24 of sum |t||b|).
+    scale = np.abs(rsa.astype(np.float64)).reshape(-1, 1) * np.abs(rsw.astype(np.float64)).reshape(1, -1)
+    upd_abs = np.abs(t_gpu) @ np.abs(lbf).T
+    bound = (bf16_ulp(base_f) + bf16_ulp(upd) + bf16_ulp(np.maximum(np.abs(ref), np.abs(got))) + rbound * scale
+             + 2.0 ** -22 * np.abs(base_f) + rank * 2.0 ** -24 * upd_abs)
     err = np.abs(got - ref)
-    assert np.all(err <= 4 * bf16_ulp(np.maximum(np.abs(ref), np.abs(got))) + 1e-30), err.max()
+    assert np.all(err <= bound), (err / bound).max()
+    assert np.mean(err <= bf16_ulp(np.abs(ref))) >= 0.99
 
 
 def test_c5_int8_full_size_bit_exact(ops, oracle, device):

@@ -35,14 +35,15 @@ def _int8_reference(oracle, x, w):
 class _Block(torch.nn.Module):
     def __init__(self, d, hidden, device):
         super().__init__()
-        lin = _mod("distributed.linear")
+        from _toy_layers import ToyColumnLinear, ToyRowLinear
+
         self.attn = torch.nn.Module()
         self.mlp = torch.nn.Module()
         kw = dict(dtype=torch.bfloat16, device=device)
-        self.attn.qkv_proj = lin.ColumnParallelLinear(d, 3 * d, bias=False, gather_output=False, **kw)
-        self.attn.out_proj = lin.RowParallelLinear(d, d, bias=True, **kw)
-        self.mlp.fc1 = lin.ColumnParallelLinear(d, hidden, bias=False, gather_output=False, **kw)
-        self.mlp.fc2 = lin.RowParallelLinear(hidden, d, bias=True, **kw)
+        self.attn.qkv_proj = ToyColumnLinear(d, 3 * d, bias=False, **kw)
+        self.attn.out_proj = ToyRowLinear(d, d, bias=True, **kw)
+        self.mlp.fc1 = ToyColumnLinear(d, hidden, bias=False, **kw)
+        self.mlp.fc2 = ToyRowLinear(hidden, d, bias=True, **kw)
 
 
 class _Transformer(torch.nn.Module):
@@ -267,9 +268,10 @@ def test_fused_lora_wrapper(oracle, device, fmt):
     result is within a few bf16 ulps of the reference's three-rounding formula."""
     lora = _mod("inference.lora")
     w8a8 = _mod("inference.w8a8")
-    lin = _mod("distributed.linear")
+    from _toy_layers import ToyColumnLinear
+
     k, n, m, rank = 512, 384, 200, 64
-    base = lin.ColumnParallelLinear(k, n, bias=False, gather_output=False, dtype=torch.bfloat16, device=device)
+    base = ToyColumnLinear(k, n, bias=False, dtype=torch.bfloat16, device=device)
     w = weights(n, k, seed=31)
     if fmt == "int8":
         qw, sw = w8a8._quantize_weight(w.to(device))
@@ -295,3 +297,106 @@ def test_fused_lora_wrapper(oracle, device, fmt):
     from _util import bf16_ulp
 
     assert np.max(np.abs(got - ref)) <= 4 * np.max(bf16_ulp(ref))
+
+
+def test_fresh_transposed_view_of_a_tiled_weight(oracle, device):
+    """A caller-made ``weight.t()`` of a tiled W8 parameter (allowed by
+    H3/inference/w8a8.py:190-220) reaches the GEMM with the tiled layout:
+    the layout is recorded against the storage, so every view carries it.
+    A row-major call on that storage raises instead of reading tiled bytes."""
+    w8a8 = _mod("inference.w8a8")
+    k, n = 1024, 512
+    m = torch.nn.Module()
+    m.weight = torch.nn.Parameter(torch.empty(n, k, dtype=torch.bfloat16, device=device))
+    m.bias = None
+    w8a8.prepare_cutlass_w8a8_stream_load_slot_(m, name="blocks.2.mlp.fc1")
+    w = weights(n, k, seed=41)
+    w8a8.load_cutlass_w8a8_stream_weight_(m, w, name="blocks.2.mlp.fc1")
+    assert ops_mod.is_tiled(m.weight) and ops_mod.is_tiled(m.weight.t()) and ops_mod.is_tiled(m.weight.data)
+    x = activations(300, k, seed=42, outlier_channels=3)
+    ref = _int8_reference(oracle, x, w)
+    ws = w8a8.CutlassW8A8Workspace()
+    for weight_t in (m.weight.t(), m.weight.detach().t(), None):
+        out = w8a8.cutlass_w8a8_linear(x.to(device), m.weight, m._cutlass_w8a8_weight_scale, bias=None,
+                                       workspace=ws, weight_t=weight_t, weight_scale_t=None)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(bits16(out), ref)
+    qa, sa = ops_mod.quant_rows(x.to(device), ops_mod.FMT_INT8, ops_mod.ROUND_RCP_MUL)
+    with pytest.raises(ValueError, match="tiled codes"):
+        ops_mod.scaled_mm(qa, m.weight.detach(), sa.reshape(-1), m._cutlass_w8a8_weight_scale.reshape(-1))
+    # a copy is a new storage of row-major meaning: no tiled mark travels with it
+    assert not ops_mod.is_tiled(m.weight.detach().clone())
+
+
+def test_fl_w8a8_torch_first_api(oracle, device):
+    """FL's twin (FL/inference/w8a8.py): post-load BF16 -> W8 conversion of the
+    selected interior projections (validated before any change), the torch-first
+    linear and workspace, and the streamed slot for a preallocated int8 weight."""
+    fl = _mod("inference.fl_w8a8")
+    assert fl.H3_CUTLASS_W8A8_POLICIES == ("interior_fc1_qkv_v1",)
+    model = _Transformer(device=device)
+    sources = {n: model.get_submodule(n).weight.detach().cpu().clone()
+               for n in ("blocks.2.attn.qkv_proj", "blocks.3.mlp.fc1")}
+    receipt = fl.quantize_h3_interior_qkv_fc1_linears_cutlass_w8a8_(torch, model, policy="interior_fc1_qkv_v1")
+    assert receipt["linear_count"] == 4 and receipt["stream_load_linear_count"] == 0
+    assert receipt["eligible_linear_count"] == 21 and receipt["bf16_boundary_block_indices"] == [0, 1, 4, 5, 6]
+    assert receipt["quantized_linear_names"] == ["blocks.2.attn.qkv_proj", "blocks.2.mlp.fc1",
+                                                 "blocks.3.attn.qkv_proj", "blocks.3.mlp.fc1"]
+    assert 0.0 < receipt["eligible_weight_fraction"] < 1.0
+    for name, w in sources.items():
+        module = model.get_submodule(name)
+        rq, rs = oracle.quant_rows(bits16(w), "int8", "div")
+        assert ops_mod.is_tiled(module.weight)
+        np.testing.assert_array_equal(bits8(module.weight), to_tiled(rq.view(np.uint8)))
+        np.testing.assert_array_equal(module._cutlass_w8a8_weight_scale.cpu().numpy().ravel(), rs)
+    # a repeated conversion finds complete storage... of the wrong kind: nothing changes
+    with pytest.raises(RuntimeError, match="incomplete CUTLASS W8A8 storage"):
+        fl.quantize_h3_interior_qkv_fc1_linears_cutlass_w8a8_(torch, model, policy="interior_fc1_qkv_v1")
+    fc1 = model.get_submodule("blocks.3.mlp.fc1")
+    x = activations(2 * 70, 256, seed=43, outlier_channels=2).reshape(2, 70, 256)
+    out = fl.cutlass_w8a8_linear(torch, x.to(device), fc1.weight, fc1._cutlass_w8a8_weight_scale, bias=None)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits16(out).reshape(-1, 512),
+                                  _int8_reference(oracle, x.reshape(-1, 256), sources["blocks.3.mlp.fc1"]))
+    ws_receipt = fl.enable_h3_cutlass_w8a8_workspace_(torch, model)
+    assert ws_receipt["linear_count"] == 4 and ws_receipt["arithmetic_order_changed"] is False
+    out_ws = model.get_submodule("blocks.3.mlp.fc1")(x.to(device))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits16(out_ws), bits16(out))
+    # streamed slot on a preallocated, frozen int8 weight (FL layers allocate it at construction)
+    slot = torch.nn.Module()
+    slot.weight = torch.nn.Parameter(torch.empty(64, 256, dtype=torch.int8, device=device), requires_grad=False)
+    slot.bias = None
+    fl.prepare_cutlass_w8a8_stream_load_slot_(torch, slot, name="blocks.2.mlp.fc1")
+    src = weights(64, 256, seed=44)
+    fl.load_cutlass_w8a8_stream_weight_(torch, slot, src, name="blocks.2.mlp.fc1", maximum_temporary_bytes=4096)
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_rows(bits16(src), "int8", "div")
+    np.testing.assert_array_equal(bits8(slot.weight), to_tiled(rq.view(np.uint8)))
+    np.testing.assert_array_equal(slot._cutlass_w8a8_weight_scale.cpu().numpy().ravel(), rs)
+    with pytest.raises(RuntimeError, match="already owns CUTLASS W8A8 storage"):
+        fl.prepare_cutlass_w8a8_stream_load_slot_(torch, slot, name="blocks.2.mlp.fc1")
+
+
+def test_lora_adapter_switch_on_a_quantized_base(device):
+    """With the adapter switched off the wrapper returns exactly the W8A8 base output."""
+    lora = _mod("inference.lora")
+    w8a8 = _mod("inference.w8a8")
+    from _toy_layers import ToyColumnLinear
+
+    k, n, rank = 512, 256, 32
+    base = ToyColumnLinear(k, n, bias=False, dtype=torch.bfloat16, device=device)
+    qw, sw = w8a8._quantize_weight(weights(n, k, seed=45).to(device))
+    base.weight = torch.nn.Parameter(qw, requires_grad=False)
+    base.register_buffer("_cutlass_w8a8_weight_scale", sw, persistent=False)
+    gen = torch.Generator().manual_seed(46)
+    la = (torch.randn(rank, k, generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    lb = (torch.randn(n, rank, generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    wrapped = lora.H3InferenceParallelLinearLoRA(base, kind="column", a=la, b=lb, scale=1.0)
+    x = activations(96, k, seed=47, outlier_channels=2).to(device)
+    with_adapter = wrapped(x)
+    wrapped.adapter_enabled = False
+    without = wrapped(x)
+    torch.cuda.synchronize()
+    assert torch.equal(without, base(x))
+    assert not torch.equal(with_adapter, without)

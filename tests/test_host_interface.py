@@ -117,45 +117,60 @@ def test_fl_dispatch_rejects_two_quantizers():
 
 
 def test_bf16_module_linear_is_plain_linear():
-    m = linear.ColumnParallelLinear(16, 8, bias=True, gather_output=False, dtype=torch.float32)
+    from _toy_layers import ToyColumnLinear
+
+    m = ToyColumnLinear(16, 8, bias=True, dtype=torch.float32)
     torch.nn.init.normal_(m.weight)
     torch.nn.init.normal_(m.bias)
     x = torch.randn(3, 16)
     assert torch.allclose(m(x), torch.nn.functional.linear(x, m.weight, m.bias))
 
 
-def test_tensor_parallel_context_slices_locally_and_refuses_exchanges():
-    """A rank of a TP=2 context holds its shard; gathering or reducing across
-    ranks is outside the single-GPU build."""
-    with pytest.raises(ValueError):
-        linear.ParallelContext(tp_world_size=2, tp_rank=2)
-    ctx = linear.ParallelContext(tp_world_size=2, tp_rank=1)
-    col = linear.ColumnParallelLinear(4, 6, bias=True, gather_output=False, dtype=torch.float32, context=ctx)
-    full = torch.arange(24, dtype=torch.float32).reshape(6, 4)
-    assert torch.equal(col.full_weight_slice(full), full[3:])
-    assert torch.equal(col.full_bias_slice(torch.arange(6.0)), torch.arange(3.0, 6.0))
-    merged = linear.MergedColumnParallelLinear(4, [2, 4], bias=False, gather_output=False, dtype=torch.float32,
-                                               context=ctx)
-    assert torch.equal(merged.full_weight_slice(full), torch.cat([full[1:2], full[4:6]]))
-    row = linear.RowParallelLinear(4, 6, bias=False, dtype=torch.float32, context=ctx)
-    assert torch.equal(row.full_weight_slice(full), full[:, 2:])
-    with torch.no_grad():
-        col.weight.copy_(col.full_weight_slice(full))
-        col.bias.zero_()
-        row.weight.copy_(row.full_weight_slice(full))
-    x = torch.randn(2, 4)
-    assert torch.allclose(col(x), x @ full[3:].t())
-    gathered = linear.ColumnParallelLinear(4, 6, bias=False, gather_output=True, dtype=torch.float32, context=ctx)
+def test_lora_wrapper_switch_and_cross_rank_guard():
+    """adapter_enabled off returns the base output alone (FL/inference/lora_checkpoint.py:452-489);
+    a row-parallel base split over ranks raises instead of returning a partial."""
+    from _toy_layers import ToyColumnLinear, ToyRowLinear
+    from taomate_h3_amd.inference import lora
+
+    base = ToyColumnLinear(16, 8, bias=False, dtype=torch.float32)
+    torch.nn.init.normal_(base.weight)
+    a, b = torch.randn(4, 16), torch.randn(8, 4)
+    wrapped = lora.H3InferenceParallelLinearLoRA(base, kind="column", a=a, b=b, scale=0.5)
+    x = torch.randn(3, 16)
+    assert torch.allclose(wrapped(x), base(x) + (x @ a.t() @ b.t()) * 0.5, atol=1e-5)
+    wrapped.adapter_enabled = False
+    assert torch.equal(wrapped(x), base(x))
+    row = ToyRowLinear(16, 8, bias=False, dtype=torch.float32, tp=(2, 1))
+    torch.nn.init.normal_(row.weight)
+    wrapped_row = lora.H3InferenceParallelLinearLoRA(row, kind="row", a=torch.randn(4, 8), b=b, scale=1.0)
     with pytest.raises(NotImplementedError, match="across tensor-parallel ranks"):
-        gathered(x)
-    with pytest.raises(NotImplementedError, match="across tensor-parallel ranks"):
-        row(torch.randn(2, 2))
+        wrapped_row(torch.randn(3, 8))
 
 
-def test_merged_column_weight_slice_keeps_logical_order():
-    m = linear.MergedColumnParallelLinear(4, [2, 3], bias=False, gather_output=False, dtype=torch.float32)
-    full = torch.arange(20, dtype=torch.float32).reshape(5, 4)
-    assert torch.equal(m.full_weight_slice(full), full)
+def test_lora_merge_and_base_model_bypass():
+    """FL's merge (fp32 delta, one rounding to the base dtype) and the
+    base-model context that switches adapters off and restores them."""
+    from _toy_layers import ToyColumnLinear
+    from taomate_h3_amd.inference import lora
+
+    root = torch.nn.Module()
+    root.proj = ToyColumnLinear(16, 8, bias=False, dtype=torch.bfloat16)
+    torch.nn.init.normal_(root.proj.weight)
+    w0 = root.proj.weight.detach().clone()
+    a = torch.randn(4, 16).to(torch.bfloat16)
+    b = torch.randn(8, 4).to(torch.bfloat16)
+    root.proj = lora.H3InferenceParallelLinearLoRA(root.proj, kind="column", a=a, b=b, scale=0.25)
+    with lora.h3_base_model_inference(root):
+        assert root.proj.adapter_enabled is False
+    assert root.proj.adapter_enabled is True
+    receipt = lora.merge_h3_lora_weights_(root)
+    expect = (w0.float() + (b.float() @ a.float()) * 0.25).to(torch.bfloat16)
+    assert torch.equal(root.proj.base.weight, expect)
+    assert receipt["target_count"] == 1 and receipt["reversible"] is False
+    assert root.proj.adapter_enabled is False and not hasattr(root.proj, "lora_a")
+    with pytest.raises(lora.H3LoRACheckpointError, match="already merged"):
+        with lora.h3_base_model_inference(root):
+            pass
 
 
 def test_ops_reject_host_tensors_before_launch():

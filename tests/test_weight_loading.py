@@ -25,9 +25,9 @@ HEADS, HEAD_DIM, HIDDEN, FFN = 4, 32, 256, 512
 
 
 def _mods():
-    import taomate_h3_amd.distributed.linear as linear
+    import _toy_layers as toy
     import taomate_h3_amd.weight_loading as wl
-    return linear, wl
+    return toy, wl
 
 
 class _Arch:
@@ -35,25 +35,22 @@ class _Arch:
     attention_head_dim = HEAD_DIM
 
 
-def _model(ctx, device, blocks=2):
-    linear, _ = _mods()
+def _model(tp, device, blocks=2):
+    toy, _ = _mods()
 
     class Attn(torch.nn.Module):
         def __init__(self):
             super().__init__()
-            self.qkv_proj = linear.MergedColumnParallelLinear(HIDDEN, [HEADS * HEAD_DIM] * 3, bias=False,
-                                                              gather_output=False, dtype=torch.bfloat16, context=ctx,
-                                                              device=device)
-            self.out_proj = linear.RowParallelLinear(HEADS * HEAD_DIM, HIDDEN, bias=True, dtype=torch.bfloat16,
-                                                     context=ctx, device=device)
+            self.qkv_proj = toy.ToyMergedColumnLinear(HIDDEN, [HEADS * HEAD_DIM] * 3, bias=False,
+                                                      dtype=torch.bfloat16, tp=tp, device=device)
+            self.out_proj = toy.ToyRowLinear(HEADS * HEAD_DIM, HIDDEN, bias=True, dtype=torch.bfloat16, tp=tp,
+                                             device=device)
 
     class Mlp(torch.nn.Module):
         def __init__(self):
             super().__init__()
-            self.fc1 = linear.ColumnParallelLinear(HIDDEN, FFN, bias=False, gather_output=False,
-                                                   dtype=torch.bfloat16, context=ctx, device=device)
-            self.fc2 = linear.RowParallelLinear(FFN, HIDDEN, bias=True, dtype=torch.bfloat16, context=ctx,
-                                                device=device)
+            self.fc1 = toy.ToyColumnLinear(HIDDEN, FFN, bias=False, dtype=torch.bfloat16, tp=tp, device=device)
+            self.fc2 = toy.ToyRowLinear(FFN, HIDDEN, bias=True, dtype=torch.bfloat16, tp=tp, device=device)
 
     class Block(torch.nn.Module):
         def __init__(self):
@@ -139,11 +136,10 @@ def test_reorder_grouped_qkv_matches_hand_layout():
 
 @pytest.mark.parametrize("index", [True, False])
 def test_bf16_load_of_a_tp_rank(tmp_path, index):
-    linear, wl = _mods()
+    _, wl = _mods()
     full, pieces = _checkpoint()
     _write(tmp_path, full, index=index)
-    ctx = linear.ParallelContext(tp_world_size=2, tp_rank=1)
-    model = _model(ctx, "cpu")
+    model = _model((2, 1), "cpu")
     receipt = wl.load_minimax_h3_dit_weights(model, tmp_path)
     expect = _expected_local(full, pieces, rank=1, tp=2)
     state = model.state_dict()
@@ -154,10 +150,38 @@ def test_bf16_load_of_a_tp_rank(tmp_path, index):
     assert model._native_weight_load_receipt is receipt
 
 
-def test_index_and_inventory_errors(tmp_path):
-    linear, wl = _mods()
+def test_fp32_parameters_and_buffers_are_checked(tmp_path):
+    """H3/model/weight_loading.py:246-251: named parameters and buffers must
+    still be fp32 after the load; the name sets default to the constants of
+    the module that defines the model class, or are passed in."""
+    _, wl = _mods()
     full, _ = _checkpoint(blocks=1)
-    model = _model(linear.ParallelContext(), "cpu", blocks=1)
+    _write(tmp_path, full, shards=1)
+    model = _model((1, 0), "cpu", blocks=1)
+    model.register_buffer("inv_freq", torch.ones(4, dtype=torch.float32), persistent=False)
+    wl.load_minimax_h3_dit_weights(model, tmp_path, fp32_param_names={"blocks.0.scale_shift_table"},
+                                   fp32_buffer_names={"inv_freq"})
+    with pytest.raises(wl.H3NativeWeightError, match="parameter must stay fp32: blocks.0.mlp.fc1.weight"):
+        wl.load_minimax_h3_dit_weights(model, tmp_path, fp32_param_names={"blocks.0.mlp.fc1.weight"})
+    model.inv_freq = model.inv_freq.to(torch.bfloat16)
+    with pytest.raises(wl.H3NativeWeightError, match="buffer must stay fp32: inv_freq"):
+        wl.load_minimax_h3_dit_weights(model, tmp_path, fp32_buffer_names={"inv_freq"})
+    # default: the name sets of the module defining the model class
+    import sys
+
+    this = sys.modules[type(model).__module__]
+    this.MINIMAX_H3_FP32_BUFFER_NAMES = frozenset({"inv_freq"})
+    try:
+        with pytest.raises(wl.H3NativeWeightError, match="buffer must stay fp32"):
+            wl.load_minimax_h3_dit_weights(model, tmp_path)
+    finally:
+        del this.MINIMAX_H3_FP32_BUFFER_NAMES
+
+
+def test_index_and_inventory_errors(tmp_path):
+    _, wl = _mods()
+    full, _ = _checkpoint(blocks=1)
+    model = _model((1, 0), "cpu", blocks=1)
     with pytest.raises(wl.H3NativeWeightError, match="cannot resolve"):
         wl.load_minimax_h3_dit_weights(model, tmp_path / "absent")
     (tmp_path / "file").write_text("")
@@ -193,12 +217,12 @@ def test_streamed_w8a8_slots_match_the_oracle(tmp_path, oracle, device):
     """W8 slots on qkv_proj (grouped reorder + merged TP slice) and fc1
     (column slice), rank 1 of TP=2, 4 KiB of staging: codes and scales equal
     the oracle's quantizer of the reference's local weights."""
-    linear, wl = _mods()
+    _, wl = _mods()
     from taomate_h3_amd.inference import w8a8
 
     full, pieces = _checkpoint()
     _write(tmp_path, full)
-    model = _model(linear.ParallelContext(tp_world_size=2, tp_rank=1), device)
+    model = _model((2, 1), device)
     slots = ["blocks.1.attn.qkv_proj", "blocks.0.mlp.fc1", "blocks.1.mlp.fc1"]
     for name in slots:
         w8a8.prepare_cutlass_w8a8_stream_load_slot_(model.get_submodule(name), name=name)
