@@ -113,6 +113,22 @@ int h3q_quant_tensor_e4m3(const void* x, int64_t rows, int64_t cols, int64_t ldx
                           float* partial, void* codes, int64_t ldq, float* scale_out, void* stream);
 
 /*
+ * h3q_quant_tensor_e4m3 without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference.  The
+ * partial maxima go to a static 4 KiB device array of the library (1024
+ * floats, one copy per GPU, held until the process ends; the current
+ * device's copy is used, so make the stream's device current), which holds every
+ * partial of any shape the kernels launch; a request needing more is refused
+ * with H3Q_ERR_UNSUPPORTED.  Nothing is allocated and nothing needs clearing.
+ * All calls on one GPU share the array: calls that overlap in time on one GPU
+ * (different streams, or other threads) race and must be serialised by the
+ * caller.  Results are those of h3q_quant_tensor_e4m3 bit for bit.
+ */
+int h3q_quant_tensor_e4m3_noalloc(const void* x, int64_t rows, int64_t cols, int64_t ldx, const float* static_scale,
+                                  void* codes, int64_t ldq, float* scale_out, void* stream);
+
+/*
  * The same quantizer with the quotient bf16(x / bf16(s)) (IEEE division by the
  * scale rounded to bf16), *scale_out = s unchanged: the reference's eager
  * expression clamp(value / scale, +-448).to(float8_e4m3fn) as torch evaluates

@@ -7,6 +7,8 @@
 // butterfly wave reduction, one IEEE reciprocal per row, then a 3-op
 // correctly rounded quotient per element and 8-byte coalesced code stores.
 // Algorithmic traffic: 2*K read + K written + 4 bytes of scale per row.
+#include <mutex>
+
 #include "h3q_common.hpp"
 #include "h3q_kernels.hpp"
 #include "row_quant.hpp"
@@ -332,6 +334,34 @@ hipError_t launch_tensor_vec(const uint16_t* x, int64_t ldx, int64_t rows, int64
 int64_t tensor_quant_parts(int64_t rows, int64_t k) {
     (void)k;
     return rows < 1 ? 1 : (rows < kTensorBlocks ? rows : kTensorBlocks);
+}
+
+// Scratch of the allocation-free per-tensor quantizer: room for the partial
+// maxima of any call (at most kTensorBlocks).  Every block of pass 1 writes
+// its own entry before pass 2 reads it, so nothing needs clearing between
+// calls; two calls that overlap on one GPU share it and race.  Each device
+// holds its own copy; host code must use the device address from
+// tensor_scratch(), never the symbol itself.
+static __device__ __align__(256) float scratch[kTensorScratchFloats];
+static_assert(kTensorScratchFloats >= kTensorBlocks, "scratch holds every partial maximum");
+
+hipError_t tensor_scratch(float** out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex lock;
+    static float* addresses[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> guard(lock);
+    if (!addresses[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));  // the current device's copy
+        if (e != hipSuccess) return e;
+        addresses[dev] = (float*)ptr;
+    }
+    *out = addresses[dev];
+    return hipSuccess;
 }
 
 hipError_t launch_quant_tensor_e4m3(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k,

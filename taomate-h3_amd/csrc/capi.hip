@@ -211,6 +211,23 @@ __attribute__((visibility("default"))) int h3q_quant_tensor_e4m3(const void* x, 
                              scale_out, stream);
 }
 
+__attribute__((visibility("default"))) int h3q_quant_tensor_e4m3_noalloc(const void* x, int64_t rows,
+                                                                         int64_t cols, int64_t ldx,
+                                                                         const float* static_scale, void* codes,
+                                                                         int64_t ldq, float* scale_out,
+                                                                         void* stream) {
+    const char* who = "h3q_quant_tensor_e4m3_noalloc";
+    if (rows > 0 && cols > 0 && h3q::tensor_quant_parts(rows, cols) > h3q::kTensorScratchFloats)
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: %lld partial maxima exceed the %lld-float scratch", who,
+                    (long long)h3q::tensor_quant_parts(rows, cols), (long long)h3q::kTensorScratchFloats);
+    float* scratch = nullptr;
+    if (rows > 0 && cols > 0 && !static_scale) {
+        const hipError_t e = h3q::tensor_scratch(&scratch);
+        if (e != hipSuccess) return fail(H3Q_ERR_HIP, "%s: scratch address: %s", who, hipGetErrorString(e));
+    }
+    return quant_tensor_e4m3(who, x, rows, cols, ldx, static_scale, false, scratch, codes, ldq, scale_out, stream);
+}
+
 __attribute__((visibility("default"))) int h3q_quant_tensor_e4m3_bf16_divisor(const void* x, int64_t rows,
                                                                               int64_t cols, int64_t ldx,
                                                                               const float* static_scale,

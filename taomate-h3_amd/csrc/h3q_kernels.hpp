@@ -17,6 +17,11 @@ hipError_t launch_quant_rows_tiled(const uint16_t* x, int64_t ldx, int64_t rows,
 
 int64_t tensor_quant_parts(int64_t rows, int64_t k);
 
+// Device address of the per-tensor quantizer's static scratch on the current
+// device (kTensorScratchFloats floats, looked up once per device).
+constexpr int64_t kTensorScratchFloats = 1024;
+hipError_t tensor_scratch(float** out);
+
 hipError_t launch_quant_tensor_e4m3(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k,
                                     const float* static_scale, bool bf16_divisor, float* partial, uint8_t* q,
                                     int64_t ldq, float* scale_out, hipStream_t st);
