@@ -25,6 +25,7 @@ extern "C" {
 /* Code formats. */
 #define H3Q_FMT_E4M3FN 0 /* OCP float8 e4m3fn, largest finite 448 */
 #define H3Q_FMT_INT8 1   /* symmetric int8 */
+#define H3Q_OUT_F16 0x100 /* h3q_scaled_mm format flag: binary16 output and bias */
 
 /* Rounding forms of the per-row quantizer. */
 #define H3Q_ROUND_DIV 0     /* q = round(x / s), s = max(amax * RN(1/L), 1e-12)  (reference weight quantizer) */
@@ -113,6 +114,31 @@ int h3q_quant_tensor_e4m3(const void* x, int64_t rows, int64_t cols, int64_t ldx
                           float* partial, void* codes, int64_t ldq, float* scale_out, void* stream);
 
 /*
+ * Per-tensor e4m3fn of a bf16, fp16 or fp32 tensor (dtype: H3Q_DTYPE_*), in
+ * either form of the reference (form):
+ *   H3Q_QUOTIENT_EAGER   torch's clamp(x / s, -448, 448) evaluated in x's
+ *                        dtype (FL/inference/fused_kernels.py:773,
+ *                        FL/inference/fp8.py:107-113): divisor and quotient
+ *                        rounded to bf16 / fp16 for those inputs, neither
+ *                        for fp32;
+ *   H3Q_QUOTIENT_TRITON  bf16(x / s) with the fp32 divisor, whatever the
+ *                        input (FL/inference/fused_kernels.py:240-246).
+ * The scale, workspace and results are those of h3q_quant_tensor_e4m3 (bf16
+ * input takes the same kernels).  A quotient 0 / 0 (fp16 divisor rounded to
+ * zero, i.e. an all-zero fp16 tensor in the eager form) gives the NaN code
+ * 0x7F, as the reference does.  fp16 and fp32 inputs
+ * run an elementwise kernel.
+ */
+#define H3Q_DTYPE_BF16 0
+#define H3Q_DTYPE_F16 1
+#define H3Q_DTYPE_F32 2
+#define H3Q_QUOTIENT_EAGER 0
+#define H3Q_QUOTIENT_TRITON 1
+int h3q_quant_tensor_e4m3_typed(const void* x, int dtype, int form, int64_t rows, int64_t cols, int64_t ldx,
+                                const float* static_scale, float* partial, void* codes, int64_t ldq,
+                                float* scale_out, void* stream);
+
+/*
  * h3q_quant_tensor_e4m3 without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid allocation).  No counterpart in the reference.  The
@@ -185,9 +211,12 @@ int h3q_quant_per_head_e4m3(const void* x, int64_t batch, int64_t seq, int64_t h
  *                     [+ lora_scale * sum_r lora_t[m, r] * lora_b[n, r]] )
  * a: codes [m, k] (lda bytes), b: weight codes [n, k] (ldb bytes, the
  * nn.Linear layout, i.e. cutlass_scaled_mm's B = weight.t()), format E4M3FN
- * or INT8 for both.  a_layout / b_layout: H3Q_LAYOUT_ROWS, or
- * H3Q_LAYOUT_TILED (k % 128 == 0; the leading dimension is then ignored;
- * tiled activations only for m <= 128 without LoRA).  Tiled weights are the
+ * or INT8 for both; format | H3Q_OUT_F16 makes out and bias IEEE binary16
+ * (one rounding of the fp32 result, torch._scaled_mm(out_dtype=float16),
+ * FL/inference/fp8.py:135-143) instead of bf16 (not with LoRA).  a_layout / b_layout:
+ * H3Q_LAYOUT_ROWS, or H3Q_LAYOUT_TILED (k % 128 == 0; the leading dimension
+ * is then ignored; tiled activations without LoRA, and for m > 128 only with
+ * k >= 256, n and ldo multiples of 8 and a 16-byte aligned out).  Tiled weights are the
  * fast format for every m (with few rows the GEMM streams them from HBM in
  * 1 KiB loads).  a_scale_kind / b_scale_kind: H3Q_SCALE_PER_ROW or
  * H3Q_SCALE_PER_TENSOR.  bias: bf16 [n] or NULL (added as one fused

@@ -31,7 +31,10 @@
  *   orc_gemm_e4m3_mfma         the same dot product under the measured accumulation
  *                              model of the gfx950 FP8 matrix instruction, with a
  *                              bound on its remaining (combination) rounding
- *   orc_epilogue_*             s_a * (s_w * float(acc)) [+ bias] -> bf16 RNE
+ *   orc_quant_tensor_e4m3_typed the same for bf16 / fp16 / fp32 input, eager form in
+ *                              the input's dtype (FL/inference/fp8.py:107-113) or Triton form
+ *   orc_f16_to_f32, orc_f32_to_f16  IEEE binary16 conversions (round to nearest even)
+ *   orc_epilogue_*             s_a * (s_w * float(acc)) [+ bias] -> bf16 RNE (or fp16)
  *   orc_rms_norm_modulate      H3/inference/fused_kernels.py:287-317 (RMSNorm + AdaLN
  *                              modulate) and :319-357 (with the residual gate), with
  *                              the sum-of-squares order and the IEEE rsqrt that the
@@ -74,6 +77,42 @@ ORC_API uint16_t orc_f32_to_bf16(float f) {
     float rf = (float)r;                           /* exact or overflow to inf */
     uint32_t rb = bits_from_f32(rf) | (b & 0x80000000u);
     return (uint16_t)(rb >> 16);
+}
+
+/* ------------------------------------------------------------------ fp16 */
+
+/* IEEE binary16: 1 sign, 5 exponent (bias 15), 10 mantissa bits. */
+ORC_API float orc_f16_to_f32(uint16_t h) {
+    int s = h >> 15, e = (h >> 10) & 31, m = h & 1023;
+    double v;
+    if (e == 31) return m ? f32_from_bits(0x7FC00000u | ((uint32_t)s << 31)) : (s ? -INFINITY : INFINITY);
+    v = (e == 0) ? ldexp((double)m, -24) : ldexp(1.0 + m / 1024.0, e - 15);
+    return (float)(s ? -v : v);
+}
+
+/* Round a binary32 value to binary16, to nearest with ties to even, on the
+ * exact binary64 value: quantum 2^(e-10) for exponent e >= -14, 2^-24 below;
+ * a magnitude that rounds to 2^16 or more overflows to infinity. */
+ORC_API uint16_t orc_f32_to_f16(float f) {
+    uint16_t sign = (uint16_t)((bits_from_f32(f) >> 16) & 0x8000);
+    if (isnan(f)) return (uint16_t)(sign | 0x7E00);
+    double a = fabs((double)f);
+    if (isinf(f)) return (uint16_t)(sign | 0x7C00);
+    if (a == 0.0) return sign;
+    int e;
+    frexp(a, &e);
+    int ex = e - 1;
+    if (ex < -14) ex = -14;
+    double quantum = ldexp(1.0, ex - 10);
+    double r = nearbyint(a / quantum) * quantum;
+    if (r >= 65536.0) return (uint16_t)(sign | 0x7C00);
+    if (r == 0.0) return sign;
+    if (r < ldexp(1.0, -14)) return (uint16_t)(sign | (uint16_t)(r / ldexp(1.0, -24)));
+    int er;
+    double mr = frexp(r, &er);
+    int expo = er - 1;
+    int mant = (int)((mr * 2.0 - 1.0) * 1024.0);
+    return (uint16_t)(sign | ((expo + 15) << 10) | mant);
 }
 
 /* ---------------------------------------------------------------- e4m3fn */
@@ -311,6 +350,60 @@ ORC_API void orc_quant_tensor_e4m3(const uint16_t* x, int64_t rows, int64_t k, i
     }
 }
 
+/* Per-tensor e4m3fn of a bf16 (dtype 0), fp16 (1) or fp32 (2) tensor.
+ * eager != 0: torch's clamp(x / scale, -448, 448) in x's dtype as evaluated
+ * on the GPU (FL/inference/fused_kernels.py:773, FL/inference/fp8.py:107-113):
+ * the 0-dim fp32 scale is cast to x's dtype, the quotient is computed in
+ * binary32 and rounded to x's dtype (bf16 / fp16; fp32 / fp32 is one IEEE
+ * division).  eager == 0: the Triton kernel (:240-246), the binary32
+ * quotient by the fp32 scale rounded to bf16, whatever x's dtype.  The scale
+ * is clamp(amax(|x|).float() / 448, min=1e-12) as in orc_quant_tensor_e4m3.
+ * A NaN quotient (0 / 0 when an fp16 divisor rounds to zero) is the device's
+ * canonical positive NaN: torch.clamp keeps it and the float8 cast writes
+ * 0x7F. */
+static float typed_load(const void* x, int dtype, int64_t i) {
+    if (dtype == 0) return orc_bf16_to_f32(((const uint16_t*)x)[i]);
+    if (dtype == 1) return orc_f16_to_f32(((const uint16_t*)x)[i]);
+    return ((const float*)x)[i];
+}
+
+static float typed_round(float v, int mode) {
+    if (mode == 1) return orc_bf16_to_f32(orc_f32_to_bf16(v));
+    if (mode == 2) return orc_f16_to_f32(orc_f32_to_f16(v));
+    return v;
+}
+
+ORC_API void orc_quant_tensor_e4m3_typed(const void* x, int dtype, int eager, int64_t rows, int64_t k, int64_t ldx,
+                                         const float* static_scale, uint8_t* q, int64_t ldq, float* scale_out) {
+    float s;
+    if (static_scale) {
+        s = *static_scale;
+    } else {
+        float amax = 0.0f;
+        for (int64_t i = 0; i < rows; ++i)
+            for (int64_t j = 0; j < k; ++j) {
+                float a = fabsf(typed_load(x, dtype, i * ldx + j));
+                if (a > amax) amax = a;
+            }
+        s = amax_scale(amax, kE4M3Max);
+    }
+    *scale_out = s;
+    const int mode = !eager ? 1 : dtype == 0 ? 1 : dtype == 1 ? 2 : 0;
+    const float d = eager ? typed_round(s, mode) : s;
+    for (int64_t i = 0; i < rows; ++i)
+        for (int64_t j = 0; j < k; ++j) {
+            const float xv = typed_load(x, dtype, i * ldx + j);
+            float v = typed_round(xv / d, mode);
+            if (isnan(v)) {
+                q[i * ldq + j] = 0x7F;
+                continue;
+            }
+            if (v < -kE4M3Max) v = -kE4M3Max;
+            if (v > kE4M3Max) v = kE4M3Max;
+            q[i * ldq + j] = orc_f32_to_e4m3(v);
+        }
+}
+
 /* ----------------------------------------------------------------- GEMMs */
 
 /* acc[m][n] = sum_k a[m][k] * b[n][k], exact in int32 (|acc| <= K*128^2). */
@@ -415,32 +508,32 @@ ORC_API void orc_gemm_e4m3_mfma(const uint8_t* a, int64_t lda, const uint8_t* b,
 }
 
 /* out = bf16(s_a[m] * (s_w[n] * float(acc)) [+ bias[n]]).  With a bias the
- * final step is one fused multiply-add (the CUTLASS ScaledEpilogueBias order). */
+ * final step is one fused multiply-add (the CUTLASS ScaledEpilogueBias order).
+ * out_f16 != 0: bias and out are binary16 (torch._scaled_mm(out_dtype=
+ * float16, bias=fp16), FL/inference/fp8.py:135-143), one rounding. */
+static uint16_t epilogue_one(float acc, float sa, float sw, const uint16_t* bias, int64_t j, int out_f16) {
+    float t = sw * acc;
+    float v = bias ? fmaf(sa, t, out_f16 ? orc_f16_to_f32(bias[j]) : orc_bf16_to_f32(bias[j])) : sa * t;
+    return out_f16 ? orc_f32_to_f16(v) : orc_f32_to_bf16(v);
+}
+
 ORC_API void orc_epilogue_i32(const int32_t* acc, int64_t ldacc, const float* s_a, int s_a_per_row,
                               const float* s_w, int s_w_per_col, const uint16_t* bias,
-                              uint16_t* out, int64_t ldo, int64_t m, int64_t n) {
+                              uint16_t* out, int64_t ldo, int64_t m, int64_t n, int out_f16) {
     for (int64_t i = 0; i < m; ++i)
-        for (int64_t j = 0; j < n; ++j) {
-            float sa = s_a[s_a_per_row ? i : 0];
-            float sw = s_w[s_w_per_col ? j : 0];
-            float t = sw * (float)acc[i * ldacc + j];
-            float v = bias ? fmaf(sa, t, orc_bf16_to_f32(bias[j])) : sa * t;
-            out[i * ldo + j] = orc_f32_to_bf16(v);
-        }
+        for (int64_t j = 0; j < n; ++j)
+            out[i * ldo + j] = epilogue_one((float)acc[i * ldacc + j], s_a[s_a_per_row ? i : 0],
+                                            s_w[s_w_per_col ? j : 0], bias, j, out_f16);
 }
 
 /* Same epilogue on an exact (binary64) accumulator rounded once to binary32. */
 ORC_API void orc_epilogue_f64(const double* acc, int64_t ldacc, const float* s_a, int s_a_per_row,
                               const float* s_w, int s_w_per_col, const uint16_t* bias,
-                              uint16_t* out, int64_t ldo, int64_t m, int64_t n) {
+                              uint16_t* out, int64_t ldo, int64_t m, int64_t n, int out_f16) {
     for (int64_t i = 0; i < m; ++i)
-        for (int64_t j = 0; j < n; ++j) {
-            float sa = s_a[s_a_per_row ? i : 0];
-            float sw = s_w[s_w_per_col ? j : 0];
-            float t = sw * (float)acc[i * ldacc + j];
-            float v = bias ? fmaf(sa, t, orc_bf16_to_f32(bias[j])) : sa * t;
-            out[i * ldo + j] = orc_f32_to_bf16(v);
-        }
+        for (int64_t j = 0; j < n; ++j)
+            out[i * ldo + j] = epilogue_one((float)acc[i * ldacc + j], s_a[s_a_per_row ? i : 0],
+                                            s_w[s_w_per_col ? j : 0], bias, j, out_f16);
 }
 
 /* ------------------------------------------------- RMSNorm + AdaLN modulate */

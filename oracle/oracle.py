@@ -85,7 +85,13 @@ def _load() -> ctypes.CDLL:
     for name in ("orc_epilogue_i32", "orc_epilogue_f64"):
         fn = getattr(lib, name)
         fn.restype = None
-        fn.argtypes = [_p, _i64, _p, ctypes.c_int, _p, ctypes.c_int, _p, _p, _i64, _i64, _i64]
+        fn.argtypes = [_p, _i64, _p, ctypes.c_int, _p, ctypes.c_int, _p, _p, _i64, _i64, _i64, ctypes.c_int]
+    lib.orc_f16_to_f32.restype = ctypes.c_float
+    lib.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.orc_f32_to_f16.restype = ctypes.c_uint16
+    lib.orc_f32_to_f16.argtypes = [ctypes.c_float]
+    lib.orc_quant_tensor_e4m3_typed.restype = None
+    lib.orc_quant_tensor_e4m3_typed.argtypes = [_p, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64, _p, _p, _i64, _p]
     _lib = lib
     return lib
 
@@ -184,6 +190,39 @@ def quant_tensor_e4m3(x_bits: np.ndarray, static_scale: float | None = None,
     return codes.reshape(np.shape(x_bits)), scale[0]
 
 
+_TYPED = {"bf16": 0, "f16": 1, "f32": 2}
+
+
+def quant_tensor_e4m3_typed(x: np.ndarray, dtype: str, eager: bool,
+                            static_scale: float | None = None) -> tuple[np.ndarray, np.float32]:
+    """Per-tensor e4m3fn of ``x`` (uint16 bits for "bf16" / "f16", float32
+    values for "f32"): the eager expression in x's dtype or the Triton form
+    (FL/inference/fused_kernels.py:771-820, FL/inference/fp8.py:107-113)."""
+    lib = _load()
+    x = np.ascontiguousarray(x, dtype=np.float32 if dtype == "f32" else np.uint16)
+    x2 = x.reshape(1, -1) if x.ndim == 1 else x.reshape(-1, x.shape[-1])
+    rows, k = x2.shape
+    codes = np.empty((rows, k), dtype=np.uint8)
+    scale = np.zeros(1, dtype=np.float32)
+    st = None if static_scale is None else np.array([static_scale], dtype=np.float32)
+    lib.orc_quant_tensor_e4m3_typed(_ptr(x2), _TYPED[dtype], int(eager), rows, k, k, _ptr(st), _ptr(codes), k,
+                                    _ptr(scale))
+    return codes.reshape(x.shape), scale[0]
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    """binary16 bits of binary32 values (round to nearest even), elementwise."""
+    lib = _load()
+    flat = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    return np.array([lib.orc_f32_to_f16(float(v)) for v in flat], dtype=np.uint16).reshape(np.shape(x))
+
+
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    lib = _load()
+    flat = np.ascontiguousarray(bits, dtype=np.uint16).ravel()
+    return np.array([lib.orc_f16_to_f32(int(v)) for v in flat], dtype=np.float32).reshape(np.shape(bits))
+
+
 def exp_f32(x: np.ndarray) -> np.ndarray:
     """The fused SwiGLU kernel's binary32 exp, elementwise."""
     lib = _load()
@@ -273,8 +312,10 @@ def gemm_e4m3_mfma(a: np.ndarray, b: np.ndarray) -> tuple[np.ndarray, np.ndarray
     return model, bound
 
 
-def epilogue(acc: np.ndarray, s_a: np.ndarray, s_w: np.ndarray, bias_bits: np.ndarray | None = None) -> np.ndarray:
-    """bf16 bits of s_a[m] * (s_w[n] * float(acc)) [+ bias[n] as one FMA].
+def epilogue(acc: np.ndarray, s_a: np.ndarray, s_w: np.ndarray, bias_bits: np.ndarray | None = None,
+             out_f16: bool = False) -> np.ndarray:
+    """bf16 bits of s_a[m] * (s_w[n] * float(acc)) [+ bias[n] as one FMA]
+    (fp16 bits, with an fp16 bias, when ``out_f16``).
 
     ``acc`` int32 (int8 path) or float64 (exact fp8 sum, rounded once to
     binary32).  ``s_a`` has M entries or 1 (per-tensor), ``s_w`` N or 1."""
@@ -291,7 +332,7 @@ def epilogue(acc: np.ndarray, s_a: np.ndarray, s_w: np.ndarray, bias_bits: np.nd
         acc = np.ascontiguousarray(acc, dtype=np.float64)
         fn = lib.orc_epilogue_f64
     fn(_ptr(acc), n, _ptr(s_a), int(s_a.size > 1), _ptr(s_w), int(s_w.size > 1), _ptr(bias),
-       _ptr(out), n, m, n)
+       _ptr(out), n, m, n, int(out_f16))
     return out
 
 

@@ -26,6 +26,7 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "h3q_quant_tensor_e4m3": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P]),
     "h3q_quant_tensor_e4m3_bf16_divisor": (_I, [_P, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P]),
     "h3q_quant_tensor_e4m3_noalloc": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _P]),
+    "h3q_quant_tensor_e4m3_typed": (_I, [_P, _I, _I, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _P]),
     "h3q_swiglu_quant": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I, _I, _P, _I64, _P, _P]),
     "h3q_quant_per_head_workspace_floats": (_I64, [_I64, _I64, _I64, _I64]),
     "h3q_quant_per_head_e4m3": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),

@@ -301,6 +301,66 @@ __global__ __launch_bounds__(256) void tensor_quant_any_kernel(const uint16_t* _
         for (int64_t j = threadIdx.x; j < k; j += 256) q[r * ldq + j] = (uint8_t)(tq.pack2(x[r * ldx + j]) & 0xFFu);
 }
 
+// Typed general path: bf16, fp16 or fp32 input, elementwise, a band of rows
+// per workgroup.  The quotient follows one of the reference's two forms:
+//   eager  (torch's clamp(x / s, +-448) in x's dtype, FL/inference/
+//          fused_kernels.py:773 and fp8.py:107-113): divisor and quotient
+//          rounded to x's dtype (bf16 or fp16; nothing for fp32),
+//   triton (FL/inference/fused_kernels.py:240-246): fp32 divisor, quotient
+//          rounded to bf16, whatever x's dtype.
+// A NaN quotient (0 / 0 when an fp16 divisor underflows to zero) stays NaN
+// through the clamp, as torch.clamp keeps it, and becomes 0x7F, the float8
+// cast of the device's canonical (positive) NaN.
+template <int IN>
+__device__ __forceinline__ float load_in(const void* __restrict__ x, int64_t i) {
+    if constexpr (IN == kInBF16) return __uint_as_float((uint32_t)((const uint16_t*)x)[i] << 16);
+    else if constexpr (IN == kInF16) return (float)((const _Float16*)x)[i];
+    else return ((const float*)x)[i];
+}
+
+template <int IN>
+__global__ __launch_bounds__(256) void tensor_amax_typed_kernel(const void* __restrict__ x, int64_t ldx, int64_t rows,
+                                                                int64_t k, int64_t rows_per_block,
+                                                                float* __restrict__ partial) {
+    __shared__ float red[4];
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+    const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
+    float amax = 0.0f;
+    for (int64_t r = r0; r < r1; ++r)
+        for (int64_t j = threadIdx.x; j < k; j += 256) amax = fmaxf(amax, fabsf(load_in<IN>(x, r * ldx + j)));
+    const float a = block_max4(amax, red);
+    if (threadIdx.x == 0) partial[blockIdx.x] = a;
+}
+
+template <int IN>
+__global__ __launch_bounds__(256) void tensor_quant_typed_kernel(const void* __restrict__ x, int64_t ldx, int64_t rows,
+                                                                 int64_t k, int64_t rows_per_block,
+                                                                 const float* __restrict__ partial, int nparts,
+                                                                 const float* __restrict__ static_scale, int eager,
+                                                                 uint8_t* __restrict__ q, int64_t ldq,
+                                                                 float* __restrict__ scale_out) {
+    __shared__ float red[4];
+    TensorQuant tq = tensor_scale(partial, nparts, static_scale, 0, red, scale_out);
+    // Rounding of divisor and quotient: 0 none, 1 bf16, 2 fp16.
+    const int rnd = !eager ? 1 : IN == kInBF16 ? 1 : IN == kInF16 ? 2 : 0;
+    if (eager && rnd == 1) tq.s = round_to_bf16(tq.s);
+    if (eager && rnd == 2) tq.s = (float)(_Float16)tq.s;
+    tq.r = 1.0f / tq.s;
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+    const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
+    for (int64_t r = r0; r < r1; ++r) {
+        for (int64_t j = threadIdx.x; j < k; j += 256) {
+            float v = tq.quotient(load_in<IN>(x, r * ldx + j));
+            if (rnd == 1) v = round_to_bf16(v);
+            if (rnd == 2) v = (float)(_Float16)v;
+            uint32_t code;
+            if (v != v) code = 0x7Fu;
+            else code = cvt_e4m3x2(__builtin_amdgcn_fmed3f(v, -kE4M3Max, kE4M3Max), 0.0f) & 0xFFu;
+            q[r * ldq + j] = (uint8_t)code;
+        }
+    }
+}
+
 namespace {
 
 constexpr int64_t kTensorBlocks = 1024;
@@ -392,6 +452,34 @@ hipError_t launch_quant_tensor_e4m3(const uint16_t* x, int64_t ldx, int64_t rows
     }
     hipLaunchKernelGGL(tensor_quant_any_kernel, dim3((unsigned)used), dim3(256), 0, st, x, ldx, rows, k, rpb,
                        (const float*)partial, (int)used, static_scale, (int)bf16_divisor, q, ldq, scale_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_quant_tensor_e4m3_typed(const void* x, int in, bool eager, int64_t ldx, int64_t rows, int64_t k,
+                                          const float* static_scale, float* partial, uint8_t* q, int64_t ldq,
+                                          float* scale_out, hipStream_t st) {
+    if (in == kInBF16)
+        return launch_quant_tensor_e4m3((const uint16_t*)x, ldx, rows, k, static_scale, eager, partial, q, ldq,
+                                        scale_out, st);
+    const int64_t blocks = rows < kTensorBlocks ? rows : kTensorBlocks;
+    const int64_t rpb = (rows + blocks - 1) / blocks;
+    const int64_t used = (rows + rpb - 1) / rpb;
+    if (!static_scale) {
+        if (in == kInF16)
+            hipLaunchKernelGGL(tensor_amax_typed_kernel<kInF16>, dim3((unsigned)used), dim3(256), 0, st, x, ldx, rows,
+                               k, rpb, partial);
+        else
+            hipLaunchKernelGGL(tensor_amax_typed_kernel<kInF32>, dim3((unsigned)used), dim3(256), 0, st, x, ldx, rows,
+                               k, rpb, partial);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (in == kInF16)
+        hipLaunchKernelGGL(tensor_quant_typed_kernel<kInF16>, dim3((unsigned)used), dim3(256), 0, st, x, ldx, rows, k,
+                           rpb, (const float*)partial, (int)used, static_scale, (int)eager, q, ldq, scale_out);
+    else
+        hipLaunchKernelGGL(tensor_quant_typed_kernel<kInF32>, dim3((unsigned)used), dim3(256), 0, st, x, ldx, rows, k,
+                           rpb, (const float*)partial, (int)used, static_scale, (int)eager, q, ldq, scale_out);
     return hipGetLastError();
 }
 

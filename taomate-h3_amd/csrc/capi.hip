@@ -191,15 +191,17 @@ __attribute__((visibility("default"))) int64_t h3q_quant_tensor_workspace_floats
     return h3q::tensor_quant_parts(rows, cols);
 }
 
-static int quant_tensor_e4m3(const char* who, const void* x, int64_t rows, int64_t cols, int64_t ldx,
-                             const float* static_scale, bool bf16_divisor, float* partial, void* codes, int64_t ldq,
+// in: h3q::TensorIn; eager: torch's clamp(x / s) in x's dtype (for bf16 the
+// bf16 divisor), else the fp32 divisor with the quotient rounded to bf16.
+static int quant_tensor_e4m3(const char* who, const void* x, int in, int64_t rows, int64_t cols, int64_t ldx,
+                             const float* static_scale, bool eager, float* partial, void* codes, int64_t ldq,
                              float* scale_out, void* stream) {
     if (rows <= 0 || cols <= 0) return fail(H3Q_ERR_INVALID, "%s: empty tensor has no amax", who);
     if (ldx < cols || ldq < cols) return fail(H3Q_ERR_INVALID, "%s: leading dimension below cols", who);
     if (!x || !codes || !scale_out || (!static_scale && !partial))
         return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
-    return check_launch(h3q::launch_quant_tensor_e4m3((const uint16_t*)x, ldx, rows, cols, static_scale, bf16_divisor,
-                                                      partial, (uint8_t*)codes, ldq, scale_out, (hipStream_t)stream),
+    return check_launch(h3q::launch_quant_tensor_e4m3_typed(x, in, eager, ldx, rows, cols, static_scale, partial,
+                                                            (uint8_t*)codes, ldq, scale_out, (hipStream_t)stream),
                         who);
 }
 
@@ -207,8 +209,8 @@ __attribute__((visibility("default"))) int h3q_quant_tensor_e4m3(const void* x, 
                                                                  int64_t ldx, const float* static_scale,
                                                                  float* partial, void* codes, int64_t ldq,
                                                                  float* scale_out, void* stream) {
-    return quant_tensor_e4m3("h3q_quant_tensor_e4m3", x, rows, cols, ldx, static_scale, false, partial, codes, ldq,
-                             scale_out, stream);
+    return quant_tensor_e4m3("h3q_quant_tensor_e4m3", x, h3q::kInBF16, rows, cols, ldx, static_scale, false, partial,
+                             codes, ldq, scale_out, stream);
 }
 
 __attribute__((visibility("default"))) int h3q_quant_tensor_e4m3_noalloc(const void* x, int64_t rows,
@@ -225,7 +227,8 @@ __attribute__((visibility("default"))) int h3q_quant_tensor_e4m3_noalloc(const v
         const hipError_t e = h3q::tensor_scratch(&scratch);
         if (e != hipSuccess) return fail(H3Q_ERR_HIP, "%s: scratch address: %s", who, hipGetErrorString(e));
     }
-    return quant_tensor_e4m3(who, x, rows, cols, ldx, static_scale, false, scratch, codes, ldq, scale_out, stream);
+    return quant_tensor_e4m3(who, x, h3q::kInBF16, rows, cols, ldx, static_scale, false, scratch, codes, ldq,
+                             scale_out, stream);
 }
 
 __attribute__((visibility("default"))) int h3q_quant_tensor_e4m3_bf16_divisor(const void* x, int64_t rows,
@@ -234,8 +237,23 @@ __attribute__((visibility("default"))) int h3q_quant_tensor_e4m3_bf16_divisor(co
                                                                               float* partial, void* codes,
                                                                               int64_t ldq, float* scale_out,
                                                                               void* stream) {
-    return quant_tensor_e4m3("h3q_quant_tensor_e4m3_bf16_divisor", x, rows, cols, ldx, static_scale, true, partial,
-                             codes, ldq, scale_out, stream);
+    return quant_tensor_e4m3("h3q_quant_tensor_e4m3_bf16_divisor", x, h3q::kInBF16, rows, cols, ldx, static_scale, true,
+                             partial, codes, ldq, scale_out, stream);
+}
+
+__attribute__((visibility("default"))) int h3q_quant_tensor_e4m3_typed(const void* x, int dtype, int form,
+                                                                       int64_t rows, int64_t cols, int64_t ldx,
+                                                                       const float* static_scale, float* partial,
+                                                                       void* codes, int64_t ldq, float* scale_out,
+                                                                       void* stream) {
+    const char* who = "h3q_quant_tensor_e4m3_typed";
+    if (dtype != H3Q_DTYPE_BF16 && dtype != H3Q_DTYPE_F16 && dtype != H3Q_DTYPE_F32)
+        return fail(H3Q_ERR_INVALID, "%s: unknown input dtype %d", who, dtype);
+    if (form != H3Q_QUOTIENT_EAGER && form != H3Q_QUOTIENT_TRITON)
+        return fail(H3Q_ERR_INVALID, "%s: unknown quotient form %d", who, form);
+    const int in = dtype == H3Q_DTYPE_BF16 ? h3q::kInBF16 : dtype == H3Q_DTYPE_F16 ? h3q::kInF16 : h3q::kInF32;
+    return quant_tensor_e4m3(who, x, in, rows, cols, ldx, static_scale, form == H3Q_QUOTIENT_EAGER, partial, codes,
+                             ldq, scale_out, stream);
 }
 
 __attribute__((visibility("default"))) int h3q_swiglu_quant(const void* x, int64_t ldx, int64_t rows, int64_t half,
@@ -333,6 +351,8 @@ __attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void*
                                                          int64_t lora_rank, float lora_scale, void* out,
                                                          int64_t ldo, int64_t m, int64_t n, int64_t k, void* stream) {
     const char* who = "h3q_scaled_mm";
+    const bool out_f16 = (format & H3Q_OUT_F16) != 0;
+    format &= ~H3Q_OUT_F16;
     if (format != H3Q_FMT_E4M3FN && format != H3Q_FMT_INT8)
         return fail(H3Q_ERR_INVALID, "%s: unknown format %d", who, format);
     for (int layout : {a_layout, b_layout})
@@ -350,6 +370,7 @@ __attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void*
     if ((lora_t == nullptr) != (lora_b == nullptr))
         return fail(H3Q_ERR_INVALID, "%s: lora_t and lora_b must be given together", who);
     if (lora_t) {
+        if (out_f16) return fail(H3Q_ERR_UNSUPPORTED, "%s: the LoRA epilogue writes bf16 only", who);
         if (lora_rank <= 0 || lora_rank > 128 || lora_rank % 8)
             return fail(H3Q_ERR_UNSUPPORTED, "%s: LoRA rank %lld (fused epilogue takes 8..128, multiple of 8)",
                         who, (long long)lora_rank);
@@ -362,10 +383,10 @@ __attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void*
     }
     // Tiled activations beyond the weight-streaming GEMM's rows are read by the
     // four-wave GEMM only (see w4_supported).
-    if (a_tiled && m > h3q::kSkinnyMaxM && (k < 256 || n % 8 || ldo % 8 || !aligned(out, 16)))
+    if (a_tiled && m > h3q::kSkinnyMaxM && (k < 256 || n % 8 || ldo % 8 || !aligned(out, 16) || out_f16))
         return fail(H3Q_ERR_UNSUPPORTED,
-                    "%s: tiled activations with m > %lld need k >= 256, n and ldo multiples of 8 and a 16-byte "
-                    "aligned output",
+                    "%s: tiled activations with m > %lld need k >= 256, n and ldo multiples of 8, a 16-byte "
+                    "aligned output and bf16 output",
                     who, (long long)h3q::kSkinnyMaxM);
     if (m == 0 || n == 0) return ok();
     if (!a || !b || !a_scale || !b_scale || !out) return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
@@ -392,6 +413,7 @@ __attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void*
     g.ldo = ldo;
     g.a_tiled = a_tiled;
     g.b_tiled = b_tiled;
+    g.out_f16 = out_f16;
     const int kind = format == H3Q_FMT_E4M3FN ? h3q::kOpE4M3 : h3q::kOpInt8;
     return check_launch(h3q::launch_gemm(kind, false, g, (hipStream_t)stream), who);
 }

@@ -201,7 +201,8 @@ __device__ __forceinline__ void mma_stage(const H3Q_LDS uint8_t* sa, const H3Q_L
     }
 }
 
-enum Epi : int { kEpiScaled = 0, kEpiI32 = 1, kEpiBF16 = 2 };
+// kEpiScaledF16: the scaled epilogue with binary16 bias and output.
+enum Epi : int { kEpiScaled = 0, kEpiI32 = 1, kEpiBF16 = 2, kEpiScaledF16 = 3 };
 
 // Wait until the oldest `pending + 1` copy stages of this wave have landed,
 // leaving `pending` younger stages in flight (only used while draining).
@@ -250,8 +251,10 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
     // Scales are fetched before the main loop so their latency hides behind
     // it: each lane's row scales in registers, the block's column scales and
     // bias in LDS (published by the first ring barrier).
+    constexpr bool kScaled = EPI == kEpiScaled || EPI == kEpiScaledF16;
+    constexpr bool kF16 = EPI == kEpiScaledF16;
     float sa_reg[TM];
-    if constexpr (EPI == kEpiScaled) {
+    if constexpr (kScaled) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int64_t m = m0 + wm0 + 32 * i + c32;
@@ -373,7 +376,8 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
                         const v4f sw4 = *(const H3Q_LDS v4f*)(sw_l + nl);
                         v2u b4 = {0u, 0u};
                         if (BIAS || !VEC) b4 = *(const H3Q_LDS v2u*)(bias_l + nl);
-                        const float bias[4] = {bf16_lo(b4[0]), bf16_hi(b4[0]), bf16_lo(b4[1]), bf16_hi(b4[1])};
+                        const float bias[4] = {out_lo(b4[0], kF16), out_hi(b4[0], kF16), out_lo(b4[1], kF16),
+                                               out_hi(b4[1], kF16)};
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const float t = __fmul_rn(sw4[e], (float)acc[i][j][4 * q + e]);
@@ -382,7 +386,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
                             y[e] = v;
                         }
                     }
-                    const uint32_t w0 = pack_bf16x2(y[0], y[1]), w1 = pack_bf16x2(y[2], y[3]);
+                    const uint32_t w0 = pack_out2(y[0], y[1], kF16), w1 = pack_out2(y[2], y[3], kF16);
                     if constexpr (VEC) {
                         const uint32_t off = n < p.n ? row_off + (uint32_t)n * kEs : kDrop;
                         __builtin_amdgcn_raw_buffer_store_b64(v2u{w0, w1}, ro, off, 0, 0);
@@ -602,6 +606,14 @@ hipError_t launch_persistent(const GemmArgs& a, hipStream_t st) {
 // epilogue vectors are double-buffered across that many stages).
 template <class T, int OP, bool LORA>
 hipError_t launch_scaled(const GemmArgs& a, hipStream_t st) {
+    if constexpr (!LORA) {
+        // binary16 output (no LoRA): the tile kernel's F16 epilogue
+        if (a.out_f16) {
+            if (!a.out_vec) return launch_tile<T, OP, kEpiScaledF16, false, false, false>(a, st);
+            return a.bias ? launch_tile<T, OP, kEpiScaledF16, false, true, true>(a, st)
+                          : launch_tile<T, OP, kEpiScaledF16, false, true, false>(a, st);
+        }
+    }
     if constexpr (!LORA && T::BM == 256 && T::BN == 256 && T::BK == 128) {
         if (a.out_vec && (a.k + T::BK - 1) / T::BK >= T::STAGES)
             return a.bias ? launch_persistent<T, OP, true>(a, st) : launch_persistent<T, OP, false>(a, st);

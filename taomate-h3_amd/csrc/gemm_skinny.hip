@@ -84,7 +84,7 @@ __device__ __forceinline__ void skinny_epilogue(const GemmArgs& p, const H3Q_LDS
         for (int e = 0; e < 4; ++e) {
             const bool in = n + e < p.n;
             sw[e] = in ? p.b_scale[p.b_scale_per_col ? n + e : 0] : 0.0f;
-            bias[e] = (BIAS || !VEC) && in && p.bias ? __uint_as_float((uint32_t)p.bias[n + e] << 16) : 0.0f;
+            bias[e] = (BIAS || !VEC) && in && p.bias ? out_lo(p.bias[n + e], p.out_f16) : 0.0f;
         }
         const bool has_bias = VEC ? BIAS : p.bias != nullptr;
 #pragma unroll
@@ -101,7 +101,7 @@ __device__ __forceinline__ void skinny_epilogue(const GemmArgs& p, const H3Q_LDS
                 const float v = __fmul_rn(sw[e], (float)s[e]);
                 y[e] = has_bias ? __builtin_fmaf(sa, v, bias[e]) : __fmul_rn(sa, v);
             }
-            const uint32_t w0 = pack_bf16x2(y[0], y[1]), w1 = pack_bf16x2(y[2], y[3]);
+            const uint32_t w0 = pack_out2(y[0], y[1], p.out_f16), w1 = pack_out2(y[2], y[3], p.out_f16);
             const uint32_t row_off = m < p.m ? (uint32_t)(m * ldo * 2) : kOob;
             if constexpr (VEC) {
                 const uint32_t off = (row_off != kOob && n < p.n) ? row_off + (uint32_t)(n * 2) : kOob;

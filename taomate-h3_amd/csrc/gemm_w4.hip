@@ -121,7 +121,9 @@ struct W4Op<kOpInt8> {
 
 }  // namespace
 
-template <int OP, bool BIAS, bool TA, bool TB>
+// F16: binary16 output and bias instead of bf16 (a separate instance, so the
+// bf16 epilogue carries no select).
+template <int OP, bool BIAS, bool TA, bool TB, bool F16>
 __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m, int tiles_n) {
     using acc_t = typename W4Op<OP>::acc_t;
     using frag_t = typename W4Op<OP>::frag_t;
@@ -334,14 +336,14 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
                     const float t = __fmul_rn(sw4[g16][x], agpr_read(acc[i][jj][4 * q + x]));
                     if constexpr (BIAS) {
                         const uint32_t w = b4[g16][x >> 1];
-                        y[x] = __builtin_fmaf(sa[i], t, (x & 1) ? bf16_hi(w) : bf16_lo(w));
+                        y[x] = __builtin_fmaf(sa[i], t, (x & 1) ? out_hi(w, F16) : out_lo(w, F16));
                     } else {
                         y[x] = __fmul_rn(sa[i], t);
                     }
                 }
                 // row cc of the block, columns 8 g16 + 4 gg .. + 3 of the wave
                 *(H3Q_LDS v2u*)(scratch + cc * 256 + ((g16 ^ (cc & 15)) << 4) + gg * 8) =
-                    v2u{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+                    v2u{pack_out2(y[0], y[1], F16), pack_out2(y[2], y[3], F16)};
             }
 #pragma unroll
             for (int r = 0; r < 8; ++r) {
@@ -399,6 +401,7 @@ bool w4_supported(const GemmArgs& a) {
     // 8-column bf16 stores, a 16-byte aligned output, and the 32-bit
     // block-relative offsets of the copies and stores.
     if (a.lora_t || a.k % 128 || a.k < 256 || a.n % 8 || a.ldo % 8 || (uintptr_t)a.out % 16) return false;
+    if (a.out_f16 && a.a_tiled) return false;  // binary16 output: row-major activations only
     if (a.m <= kSkinnyMaxM) return false;
     const int64_t tiled_block_row = (a.k / 128) * 2048 * 16;  // 256 rows of a tiled operand
     if ((a.a_tiled && tiled_block_row >= (int64_t(1) << 31)) || (a.b_tiled && tiled_block_row >= (int64_t(1) << 31)))
@@ -410,12 +413,15 @@ template <int OP, bool BIAS>
 static hipError_t launch_w4_op(const GemmArgs& a, hipStream_t st) {
     const int tiles_m = (int)((a.m + 255) / 256), tiles_n = (int)((a.n + 255) / 256);
     const dim3 grid((unsigned)persistent_grid(tiles_m * tiles_n));
-    if (a.a_tiled) {
-        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
-        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+    if (a.out_f16) {
+        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, true, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, false, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+    } else if (a.a_tiled) {
+        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, true, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, false, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
     } else {
-        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
-        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, true, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, false, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
     }
     return hipGetLastError();
 }

@@ -42,6 +42,27 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{lo, hi}, v2bf));
 }
 
+// Two binary32 values -> two IEEE binary16 (round to nearest even, overflow
+// to infinity) in one word, low half first.  The values are pinned as
+// binary32 first: otherwise the compiler may fold a preceding fmaf into a
+// mixed-precision FMA that rounds the exact result to binary16 once, where
+// the epilogue rounds to binary32 and then to binary16.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+    asm volatile("" : "+v"(lo), "+v"(hi));
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
+__device__ __forceinline__ float f16_lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)w); }
+__device__ __forceinline__ float f16_hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
+
+// Output elements of the scaled GEMMs (and their bias): bf16, or binary16
+// when f16 (a uniform kernel argument).
+__device__ __forceinline__ uint32_t pack_out2(float lo, float hi, bool f16) {
+    return f16 ? pack_f16x2(lo, hi) : pack_bf16x2(lo, hi);
+}
+__device__ __forceinline__ float out_lo(uint32_t w, bool f16) { return f16 ? f16_lo(w) : bf16_lo(w); }
+__device__ __forceinline__ float out_hi(uint32_t w, bool f16) { return f16 ? f16_hi(w) : bf16_hi(w); }
+
 __device__ __forceinline__ float round_to_bf16(float f) {
     return __uint_as_float(f32_to_bf16_bits(f) << 16);
 }

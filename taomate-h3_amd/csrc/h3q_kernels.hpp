@@ -22,6 +22,16 @@ int64_t tensor_quant_parts(int64_t rows, int64_t k);
 constexpr int64_t kTensorScratchFloats = 1024;
 hipError_t tensor_scratch(float** out);
 
+// Input types of the typed per-tensor quantizer (mirrored by include/taomate_h3_amd.h).
+enum TensorIn : int { kInBF16 = 0, kInF16 = 1, kInF32 = 2 };
+
+// Per-tensor e4m3 of bf16 / fp16 / fp32 input; eager: torch's clamp(x / s) in
+// x's dtype, else the fp32-divisor quotient rounded to bf16.  bf16 input runs
+// the vector kernels of launch_quant_tensor_e4m3.
+hipError_t launch_quant_tensor_e4m3_typed(const void* x, int in, bool eager, int64_t ldx, int64_t rows, int64_t k,
+                                          const float* static_scale, float* partial, uint8_t* q, int64_t ldq,
+                                          float* scale_out, hipStream_t st);
+
 hipError_t launch_quant_tensor_e4m3(const uint16_t* x, int64_t ldx, int64_t rows, int64_t k,
                                     const float* static_scale, bool bf16_divisor, float* partial, uint8_t* q,
                                     int64_t ldq, float* scale_out, hipStream_t st);
@@ -74,6 +84,7 @@ struct GemmArgs {
     int64_t ldo;            // in elements
     int out_vec;            // ldo % 4 == 0, n % 4 == 0 and out 16-byte aligned: 4 columns per store
     int a_tiled, b_tiled;   // operand stored in the tiled layout (k % 128 == 0; rows padded to 16 with zeros)
+    int out_f16;            // scaled output and bias are IEEE binary16 instead of bf16
 };
 
 // out = epilogue(A @ B^T).  kind: kOpE4M3 / kOpInt8 scaled to bf16 (with

@@ -78,6 +78,48 @@ def resolve_h3_dynamic_fp8_policy(linear_names: list[str], *, policy: str | None
     }
 
 
+# Receipt vocabulary of FL/inference/fp8.py:288-372: which projections a
+# policy covers, the reason it gives, and the components FP8 never touches.
+_PROJECTION_SETS = {
+    INTERIOR_FC1_ONLY_FP8_POLICY: "mlp_input_interior_blocks",
+    INTERIOR_FC1_MID18_QKV_FP8_POLICY: "mlp_input_interior_and_mid18_qkv_blocks",
+    QUALITY_FIRST_RESIDUAL_FP8_POLICY: "qkv_and_mlp_input_interior_blocks",
+}
+_EXCLUDED_COMPONENTS = ("lora_adapter_tensors", "patch_projections", "timestep_projections",
+                        "final_output_projections", "token_refiner", "condition_and_adaln")
+_BOUNDARY_REASON = "both representation boundaries"
+
+
+def _projection_set(policy: str | None, mlp_only: bool) -> str:
+    return "mlp_only" if mlp_only else _PROJECTION_SETS.get(policy, "attention_and_mlp")
+
+
+def _policy_rules(policy: str | None, selection: dict[str, Any]) -> dict[str, Any] | None:
+    """What a named policy quantizes and protects, for the receipt; None
+    without a named policy."""
+    if policy not in H3_DYNAMIC_FP8_POLICIES:
+        return None
+    fc1_only = policy == INTERIOR_FC1_ONLY_FP8_POLICY
+    if fc1_only:
+        reason = ("protect attention, residual-write projections, and " + _BOUNDARY_REASON
+                  + " (first two and last three blocks)")
+    elif policy in _INTERIOR_QKV_BLOCK_RANGES:
+        lo, hi = _INTERIOR_QKV_BLOCK_RANGES[policy]
+        reason = (f"protect QKV outside blocks {lo} through {hi}, all residual-write projections, and "
+                  + _BOUNDARY_REASON)
+    else:
+        reason = "protect residual-write projections and " + _BOUNDARY_REASON + " (first two and last three blocks)"
+    quantized = ["mlp.fc1"] if fc1_only else ["attn.qkv_proj", "mlp.fc1"]
+    return {
+        "quantized_projection_suffixes": quantized,
+        "bf16_projection_suffixes": [s for s in ("attn.qkv_proj", "attn.out_proj", "mlp.fc2") if s not in quantized],
+        "bf16_boundary_block_indices": selection["bf16_boundary_block_indices"],
+        "quantized_qkv_block_indices": selection["quantized_qkv_block_indices"],
+        "bf16_qkv_block_indices": selection["bf16_qkv_block_indices"],
+        "reason": reason,
+    }
+
+
 def quantize_weight_fp8_tensor(weight: Any) -> tuple[Any, Any]:
     """Per-tensor e4m3fn weight codes and 0-dim fp32 scale (FL/inference/fp8.py:259-263,
     :107-113): the eager expression as torch evaluates it on the GPU, so the
@@ -92,15 +134,22 @@ def quantize_weight_fp8_rows(weight: Any) -> tuple[Any, Any]:
 
 class FP8DynamicLinear:
     """Inference-only FP8 replacement for an aligned ``torch.nn.Linear``
-    (FL/inference/fp8.py:96-146).  The GEMM produces bf16 and the module
-    returns it cast to fp16, the reference's output dtype for this module."""
+    (FL/inference/fp8.py:96-146).
+
+    As in the reference, everything is quantized in its own dtype: the
+    source weight (bf16, fp16 or fp32; the video VAE that uses this module
+    loads fp32) with the eager expression ``clamp(w / s)`` in that dtype, the
+    activations per call by ``quantize_fp8_e4m3_dynamic`` in theirs (fp16
+    under the VAE's autocast).  The bias is kept as fp16 and the GEMM
+    rounds ``s_x * (s_w * acc) + bias`` once to fp16, as
+    ``torch._scaled_mm(..., bias=fp16, out_dtype=torch.float16)``."""
 
     @staticmethod
     def from_linear(torch: Any, source: Any) -> Any:
         class _FP8DynamicLinear(torch.nn.Module):
             def __init__(self) -> None:
                 super().__init__()
-                quantized, scale = quantize_weight_fp8_tensor(source.weight.detach().to(torch.bfloat16))
+                quantized, scale = ops.quant_tensor_e4m3(source.weight.detach().contiguous(), eager=True)
                 self.weight = torch.nn.Parameter(quantized, requires_grad=False)
                 self.register_buffer("weight_scale", scale, persistent=True)
                 self.bias = (torch.nn.Parameter(source.bias.detach().to(torch.float16), requires_grad=False)
@@ -112,12 +161,11 @@ class FP8DynamicLinear:
                 from .fused_kernels import quantize_fp8_e4m3_dynamic
 
                 shape = (*value.shape[:-1], self.out_features)
-                flattened = value.reshape(-1, self.in_features).to(torch.bfloat16)
+                flattened = value.reshape(-1, self.in_features)
                 quantized, input_scale = quantize_fp8_e4m3_dynamic(flattened)
-                bias = None if self.bias is None else self.bias.to(torch.bfloat16)
                 output = ops.scaled_mm(quantized, self.weight, input_scale.reshape(1), self.weight_scale.reshape(1),
-                                       bias=bias)
-                return output.to(torch.float16).reshape(shape)
+                                       bias=self.bias, out_dtype=torch.float16)
+                return output.reshape(shape)
 
         return _FP8DynamicLinear()
 
@@ -200,16 +248,21 @@ def _quantize_h3_block_linears_fp8_(torch: Any, transformer: Any, *, activation_
             module._fp8_activation_scale_margin = activation_scale_margin
         names.append(name)
     protected = selection["bf16_protected_linear_names"]
+    calibrated = activation_calibration_forwards is not None
     return {
         "schema": "digitalhuman_h3.inference.fp8.v3",
         "scope": "frozen_main_dit_base_weights_only",
+        "excluded_components": list(_EXCLUDED_COMPONENTS),
         "format": "float8_e4m3fn",
-        "activation_scale": ("dynamic_per_tensor" if activation_calibration_forwards is None
-                             else "calibrated_static_per_tensor"),
+        "activation_scale": "calibrated_static_per_tensor" if calibrated else "dynamic_per_tensor",
         "activation_calibration_forwards": activation_calibration_forwards,
         "activation_scale_margin": activation_scale_margin,
+        "activation_calibration_scope": "student_av_forwards_only" if calibrated else None,
+        "base_model_bypass_forwards": ("per_forward_scale_without_consuming_calibration" if calibrated else None),
         "weight_scale": "static_per_tensor",
+        "projection_set": _projection_set(policy, mlp_only),
         "policy": policy or ("mlp_only_v1" if mlp_only else "all_main_blocks_v1"),
+        "policy_rules": _policy_rules(policy, selection),
         "eligible_linear_count": len(candidates),
         "linear_count": len(names),
         "bf16_protected_linear_count": len(protected),

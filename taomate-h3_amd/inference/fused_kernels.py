@@ -71,19 +71,19 @@ def _as_bf16(value: torch.Tensor, name: str) -> torch.Tensor:
 
 
 def quantize_fp8_e4m3(value: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
-    """Static per-tensor e4m3fn codes of ``value`` with the given fp32 scale
-    (FL/inference/fused_kernels.py:771-785)."""
-    _as_bf16(value, "quantize_fp8_e4m3")
+    """Static per-tensor e4m3fn codes of a bf16, fp16 or fp32 ``value`` with
+    the given fp32 scale (FL/inference/fused_kernels.py:771-785): the eager
+    expression in value's dtype until the fused kernels are enabled, then
+    the Triton kernel's bf16-rounded fp32 quotient."""
     scale = scale.to(device=value.device, dtype=torch.float32)
-    codes, _ = ops.quant_tensor_e4m3(value.contiguous(), scale.reshape(()), bf16_divisor=not _ENABLED)
+    codes, _ = ops.quant_tensor_e4m3(value.contiguous(), scale.reshape(()), eager=not _ENABLED)
     return codes
 
 
 def quantize_fp8_e4m3_dynamic(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Dynamic per-tensor e4m3fn: (codes, 0-dim fp32 scale ``max(amax * RN(1/448), 1e-12)``)
-    (FL/inference/fused_kernels.py:788-820)."""
-    _as_bf16(value, "quantize_fp8_e4m3_dynamic")
-    return ops.quant_tensor_e4m3(value.contiguous(), bf16_divisor=not _ENABLED)
+    """Dynamic per-tensor e4m3fn of a bf16, fp16 or fp32 tensor: (codes, 0-dim
+    fp32 scale ``max(amax * RN(1/448), 1e-12)``) (FL/inference/fused_kernels.py:788-820)."""
+    return ops.quant_tensor_e4m3(value.contiguous(), eager=not _ENABLED)
 
 
 def quantize_fp8_e4m3_per_head(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

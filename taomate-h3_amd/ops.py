@@ -23,6 +23,9 @@ SCALE_PER_TENSOR = 0
 SCALE_PER_ROW = 1
 LAYOUT_ROWS = 0
 LAYOUT_TILED = 1
+OUT_F16 = 0x100      # scaled_mm format flag: binary16 output and bias
+QUOTIENT_EAGER = 0   # per-tensor quotient forms of h3q_quant_tensor_e4m3_typed
+QUOTIENT_TRITON = 1
 SKINNY_MAX_M = 128   # tiled activations (weight-streaming GEMM) up to this many rows
 
 _CODE_DTYPES = {FMT_E4M3FN: torch.float8_e4m3fn, FMT_INT8: torch.int8}
@@ -273,16 +276,25 @@ def quant_rows_tiled(x: torch.Tensor, fmt: int, rounding: int = ROUND_DIV, *, co
     return codes, scales
 
 
+_TENSOR_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
 def quant_tensor_e4m3(x: torch.Tensor, static_scale: torch.Tensor | None = None, *,
                       codes: torch.Tensor | None = None, scale: torch.Tensor | None = None,
                       workspace: torch.Tensor | None = None,
-                      bf16_divisor: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
-    """Per-tensor e4m3fn with the bf16 intermediate; returns (codes, 0-dim fp32 scale).
-    ``bf16_divisor``: divide by the scale rounded to bf16 (the reference's
-    eager expression on the GPU) instead of the fp32 scale (its Triton kernel)."""
+                      bf16_divisor: bool = False, eager: bool | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-tensor e4m3fn of a bf16, fp16 or fp32 tensor; returns (codes, 0-dim fp32 scale).
+
+    ``eager``: torch's ``clamp(x / s, -448, 448)`` evaluated in x's dtype
+    (the reference's eager expression on the GPU: for bf16 / fp16 input the
+    divisor and the quotient are rounded to that dtype, for fp32 neither);
+    otherwise the reference's Triton form, the fp32-divisor quotient rounded
+    to bf16.  For bf16 input ``bf16_divisor`` is the older name of ``eager``."""
     _require_gpu("quant_tensor_e4m3", x, static_scale, codes, scale, workspace)
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"quant_tensor_e4m3: expected bfloat16 input, got {x.dtype}")
+    if x.dtype not in _TENSOR_DTYPES:
+        raise TypeError(f"quant_tensor_e4m3: expected bfloat16, float16 or float32 input, got {x.dtype}")
+    if eager is None:
+        eager = bf16_divisor
     shape = tuple(x.shape)
     x2 = x.reshape(-1, shape[-1]) if x.ndim != 2 else x
     if x2.ndim != 2 or x2.stride(-1) != 1:
@@ -300,9 +312,14 @@ def quant_tensor_e4m3(x: torch.Tensor, static_scale: torch.Tensor | None = None,
     elif workspace is None:
         n = int(_lib.lib().h3q_quant_tensor_workspace_floats(rows, cols))
         workspace = torch.empty(n, device=x.device, dtype=torch.float32)
-    _lib.call("h3q_quant_tensor_e4m3_bf16_divisor" if bf16_divisor else "h3q_quant_tensor_e4m3", _ptr(x2), rows,
-              cols, x2.stride(0), _ptr(static_scale), _ptr(workspace),
-              _ptr(c2), c2.stride(0), _ptr(scale), _stream(x))
+    if x.dtype == torch.bfloat16:
+        _lib.call("h3q_quant_tensor_e4m3_bf16_divisor" if eager else "h3q_quant_tensor_e4m3", _ptr(x2), rows,
+                  cols, x2.stride(0), _ptr(static_scale), _ptr(workspace),
+                  _ptr(c2), c2.stride(0), _ptr(scale), _stream(x))
+    else:
+        _lib.call("h3q_quant_tensor_e4m3_typed", _ptr(x2), _TENSOR_DTYPES[x.dtype], QUOTIENT_EAGER if eager
+                  else QUOTIENT_TRITON, rows, cols, x2.stride(0), _ptr(static_scale), _ptr(workspace),
+                  _ptr(c2), c2.stride(0), _ptr(scale), _stream(x))
     return codes, scale
 
 
@@ -392,8 +409,11 @@ def scaled_mm(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor, b_scale: 
               bias: torch.Tensor | None = None, lora_t: torch.Tensor | None = None,
               lora_b: torch.Tensor | None = None, lora_scale: float = 1.0,
               out: torch.Tensor | None = None, a_tiled: bool = False, b_tiled: bool = False,
-              m: int | None = None, n: int | None = None) -> torch.Tensor:
-    """bf16 out[m, n] = a_scale[m] * (b_scale[n] * (a @ b^T)) [+ bias] [+ lora_scale * lora_t @ lora_b^T].
+              m: int | None = None, n: int | None = None,
+              out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """out[m, n] = a_scale[m] * (b_scale[n] * (a @ b^T)) [+ bias] [+ lora_scale * lora_t @ lora_b^T],
+    rounded once to ``out_dtype`` (bf16, or float16 as torch._scaled_mm's
+    out_dtype; the bias is then float16 too).
 
     ``a`` [m, k] and ``b`` [n, k] are both e4m3fn or both int8 codes (``b`` in
     the nn.Linear [out, in] layout).  A tiled operand (``a_tiled`` /
@@ -419,9 +439,11 @@ def scaled_mm(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor, b_scale: 
     check_layout("scaled_mm b", b, b_tiled)
     ak = _scale_kind("scaled_mm a_scale", a_scale, m)
     bk = _scale_kind("scaled_mm b_scale", b_scale, n)
+    if out_dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"scaled_mm: out_dtype must be bfloat16 or float16, got {out_dtype}")
     if bias is not None:
-        if bias.dtype != torch.bfloat16 or bias.numel() != n or not bias.is_contiguous():
-            raise ValueError("scaled_mm: bias must be a contiguous bf16 vector of length n")
+        if bias.dtype != out_dtype or bias.numel() != n or not bias.is_contiguous():
+            raise ValueError(f"scaled_mm: bias must be a contiguous {out_dtype} vector of length n")
     rank = 0
     if (lora_t is None) != (lora_b is None):
         raise ValueError("scaled_mm: lora_t and lora_b go together")
@@ -432,13 +454,14 @@ def scaled_mm(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor, b_scale: 
         if lora_t.shape[0] != m or tuple(lora_b.shape) != (n, rank):
             raise ValueError("scaled_mm: LoRA shapes must be t [m, r] and B [n, r]")
     if out is None:
-        out = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
-    _rows_2d("scaled_mm out", out, torch.bfloat16)
+        out = torch.empty((m, n), device=a.device, dtype=out_dtype)
+    _rows_2d("scaled_mm out", out, out_dtype)
     if tuple(out.shape) != (m, n):
         raise ValueError(f"scaled_mm: out shape {tuple(out.shape)} != {(m, n)}")
     if m == 0 or n == 0:
         return out
-    _lib.call("h3q_scaled_mm", _FORMATS[a.dtype], _ptr(a), a.stride(0), LAYOUT_TILED if a_tiled else LAYOUT_ROWS,
+    fmt = _FORMATS[a.dtype] | (OUT_F16 if out_dtype == torch.float16 else 0)
+    _lib.call("h3q_scaled_mm", fmt, _ptr(a), a.stride(0), LAYOUT_TILED if a_tiled else LAYOUT_ROWS,
               _ptr(a_scale), ak, _ptr(b), b.stride(0), LAYOUT_TILED if b_tiled else LAYOUT_ROWS, _ptr(b_scale), bk,
               _ptr(bias), _ptr(lora_t), lora_t.stride(0) if lora_t is not None else 0,
               _ptr(lora_b), lora_b.stride(0) if lora_b is not None else 0, rank, float(lora_scale), _ptr(out),

@@ -81,6 +81,22 @@ def test_version_and_error_without_gpu():
     rc = lib.h3q_scaled_mm(0, None, 128, 5, None, 1, None, 128, 0, None, 1, None, None, 0, None, 0, 0, 1.0, None,
                            8, 4, 8, 128, None)
     assert rc == 1 and b"unknown operand layout" in lib.h3q_last_error()
+    # binary16 output (format | H3Q_OUT_F16): not with LoRA, not with tiled activations above 128 rows
+    f16 = 0x100
+    rc = lib.h3q_scaled_mm(f16, None, 128, 0, None, 1, None, 128, 0, None, 1, None, p, 128, p, 128, 128, 1.0,
+                           None, 8, 4, 8, 128, None)
+    assert rc == 2 and b"bf16 only" in lib.h3q_last_error()
+    rc = lib.h3q_scaled_mm(f16 | 1, None, 0, 1, None, 1, None, 0, 1, None, 1, None, None, 0, None, 0, 0, 1.0, None,
+                           8, 256, 8, 256, None)
+    assert rc == 2 and b"bf16 output" in lib.h3q_last_error()
+    rc = lib.h3q_scaled_mm(0x200, None, 128, 0, None, 1, None, 128, 0, None, 1, None, None, 0, None, 0, 0, 1.0, None,
+                           8, 4, 8, 128, None)
+    assert rc == 1 and b"unknown format" in lib.h3q_last_error()
+    # the typed per-tensor quantizer checks its dtype and form
+    rc = lib.h3q_quant_tensor_e4m3_typed(None, 3, 0, 4, 16, 16, None, None, None, 16, None, None)
+    assert rc == 1 and b"unknown input dtype" in lib.h3q_last_error()
+    rc = lib.h3q_quant_tensor_e4m3_typed(None, 1, 2, 4, 16, 16, None, None, None, 16, None, None)
+    assert rc == 1 and b"unknown quotient form" in lib.h3q_last_error()
     rc = lib.h3q_quant_rows_tiled(None, 4, 100, 100, 0, 0, 0, None, None, None)
     assert rc == 1 and b"multiple of 128" in lib.h3q_last_error()
     assert lib.h3q_tiled_bytes(17, 256) == 2 * 2 * 2048 and lib.h3q_tiled_bytes(16, 100) == 0

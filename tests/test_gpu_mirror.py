@@ -182,8 +182,13 @@ def test_fp8_tensor_quantizers(oracle, device, monkeypatch, fused):
     assert tuple(s3.shape) == (9, 37, 1)
     np.testing.assert_array_equal(bits8(q3).reshape(333, 1040), rq3)
     np.testing.assert_array_equal(s3.cpu().numpy().ravel(), rs3)
+    # fp32 input is quantized in its own dtype (fp32 quotient eager; bf16-rounded fused)
+    q4, s4 = fk.quantize_fp8_e4m3_dynamic(x.float().to(device))
+    rq4, rs4 = oracle.quant_tensor_e4m3_typed(x.float().numpy(), "f32", not fused)
+    np.testing.assert_array_equal(bits8(q4), rq4)
+    assert np.float32(s4.item()) == rs4
     with pytest.raises(TypeError):
-        fk.quantize_fp8_e4m3_dynamic(x.float().to(device))
+        fk.quantize_fp8_e4m3_dynamic(x.to(torch.float64).to(device))
 
 
 def test_fp8_w8a8_module_dispatch(oracle, device):
@@ -221,6 +226,10 @@ def test_fp8_per_tensor_module_dispatch(oracle, device):
     weight = fc2.weight.detach().cpu().clone()
     receipt = fp8.quantize_h3_block_linears_dynamic_fp8_(torch, model)
     assert receipt["linear_count"] == 28 and receipt["weight_scale"] == "static_per_tensor"
+    assert receipt["projection_set"] == "attention_and_mlp" and receipt["policy_rules"] is None
+    assert receipt["activation_calibration_scope"] is None and receipt["base_model_bypass_forwards"] is None
+    assert receipt["excluded_components"] == ["lora_adapter_tensors", "patch_projections", "timestep_projections",
+                                              "final_output_projections", "token_refiner", "condition_and_adaln"]
     x = activations(130, 512, seed=9, outlier_channels=3)
     # eager mode (the fused kernels not enabled): bf16 divisors on the GPU
     rqa, rsa = oracle.quant_tensor_e4m3(bits16(x), bf16_divisor=True)
@@ -241,7 +250,10 @@ def test_fp8_calibrated_scale_then_static(oracle, device):
     scale x margin is the static activation scale (FL/distributed/linear.py:104-128)."""
     fp8 = _mod("inference.fp8")
     model = _Transformer(blocks=5, device=device)
-    fp8.quantize_h3_block_linears_calibrated_fp8_(torch, model, calibration_forwards=2, scale_margin=1.25)
+    receipt = fp8.quantize_h3_block_linears_calibrated_fp8_(torch, model, calibration_forwards=2, scale_margin=1.25)
+    assert receipt["activation_calibration_scope"] == "student_av_forwards_only"
+    assert receipt["base_model_bypass_forwards"] == "per_forward_scale_without_consuming_calibration"
+    assert receipt["activation_scale"] == "calibrated_static_per_tensor"
     fc1 = model.get_submodule("blocks.1.mlp.fc1")
     xa = activations(64, 256, seed=1)
     xb = (activations(64, 256, seed=2).float() * 3).to(torch.bfloat16)

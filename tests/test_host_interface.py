@@ -52,6 +52,42 @@ def test_fp8_policies(policy, qkv_blocks, fc1):
     assert sel["bf16_boundary_block_indices"] == [0, 1, 47, 48, 49]
 
 
+def test_fp8_receipt_policy_rules_and_projection_sets():
+    """The receipt fields FL/inference/fp8.py:288-372 derives from the policy,
+    with the reference's literal strings."""
+    boundary = [0, 1, 47, 48, 49]
+    fc1_only = fp8._policy_rules("interior_fc1_only_v1",
+                                 fp8.resolve_h3_dynamic_fp8_policy(NAMES, policy="interior_fc1_only_v1"))
+    assert fc1_only == {
+        "quantized_projection_suffixes": ["mlp.fc1"],
+        "bf16_projection_suffixes": ["attn.qkv_proj", "attn.out_proj", "mlp.fc2"],
+        "bf16_boundary_block_indices": boundary,
+        "quantized_qkv_block_indices": [],
+        "bf16_qkv_block_indices": list(range(50)),
+        "reason": "protect attention, residual-write projections, and both representation boundaries "
+                  "(first two and last three blocks)",
+    }
+    mid = fp8._policy_rules("interior_fc1_mid18_qkv_v1",
+                            fp8.resolve_h3_dynamic_fp8_policy(NAMES, policy="interior_fc1_mid18_qkv_v1"))
+    assert mid["quantized_projection_suffixes"] == ["attn.qkv_proj", "mlp.fc1"]
+    assert mid["bf16_projection_suffixes"] == ["attn.out_proj", "mlp.fc2"]
+    assert mid["quantized_qkv_block_indices"] == list(range(16, 34))
+    assert mid["bf16_qkv_block_indices"] == [b for b in range(50) if not 16 <= b <= 33]
+    assert mid["reason"] == ("protect QKV outside blocks 16 through 33, all residual-write projections, "
+                             "and both representation boundaries")
+    qf = fp8._policy_rules("quality_first_residual_v1",
+                           fp8.resolve_h3_dynamic_fp8_policy(NAMES, policy="quality_first_residual_v1"))
+    assert qf["reason"] == ("protect residual-write projections and both representation boundaries "
+                            "(first two and last three blocks)")
+    assert qf["bf16_qkv_block_indices"] == boundary
+    assert fp8._policy_rules(None, fp8.resolve_h3_dynamic_fp8_policy(NAMES, policy=None)) is None
+    assert [fp8._projection_set(p, False) for p in (None, "interior_fc1_only_v1", "interior_fc1_mid18_qkv_v1",
+                                                    "quality_first_residual_v1")] == [
+        "attention_and_mlp", "mlp_input_interior_blocks", "mlp_input_interior_and_mid18_qkv_blocks",
+        "qkv_and_mlp_input_interior_blocks"]
+    assert fp8._projection_set(None, True) == "mlp_only"
+
+
 def test_fp8_policy_none_and_errors():
     assert fp8.resolve_h3_dynamic_fp8_policy(NAMES, policy=None)["quantized_linear_names"] == NAMES
     with pytest.raises(ValueError, match="unsupported H3 dynamic FP8 policy"):

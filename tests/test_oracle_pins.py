@@ -644,3 +644,105 @@ def test_norm_closed_forms(oracle):
     _, hid = oracle.rms_norm_modulate(np.zeros_like(res), weight, scale, shift, np.array([1, 1], np.int64), 1e-6,
                                       residual_gate=(br, gates))
     np.testing.assert_array_equal(hid, br)
+
+
+# ------------------------------------------- fp16 / fp32 per-tensor and fp16 output
+
+def test_f16_conversions_match_numpy(oracle):
+    """binary16 decode of every bit pattern, and round-to-nearest-even encode
+    of random, tie, subnormal and overflow-boundary binary32 values, against
+    numpy's IEEE conversions."""
+    allbits = np.arange(65536, dtype=np.uint16)
+    got = oracle.f16_to_f32(allbits)
+    ref = allbits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    rng = np.random.default_rng(5)
+    vals = np.concatenate([
+        (rng.standard_normal(20000) * np.exp2(rng.integers(-30, 17, 20000))).astype(np.float32),
+        # exact ties between neighbouring binary16 values (normal and subnormal)
+        ((np.arange(1, 2000, dtype=np.float64) + 0.5) * 2.0 ** -24).astype(np.float32),
+        ((1024 + np.arange(0, 1024) + 0.5) * 2.0 ** -10).astype(np.float32),
+        np.array([65504.0, 65519.99, 65520.0, 1e9, -65520.0, 2.0 ** -25, 2.0 ** -25 * 1.0001, 0.0, -0.0],
+                 dtype=np.float32),
+    ])
+    with np.errstate(over="ignore"):
+        ref16 = vals.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(oracle.f32_to_f16(vals), ref16)
+
+
+def _typed_inputs():
+    gen = torch.Generator().manual_seed(21)
+    x = torch.randn(40, 384, generator=gen) * torch.exp2(torch.randint(-8, 4, (1, 384), generator=gen).float())
+    x[:, 7] *= 30.0
+    return x
+
+
+@pytest.mark.parametrize("static", [None, 0.0371])
+def test_typed_tensor_quant_matches_torch_with_explicit_divisors(oracle, static):
+    """The eager expression clamp(x / s) as torch evaluates it on the GPU:
+    fp16 input divides by fp16(s) and rounds the quotient to fp16; fp32 input
+    is one IEEE division.  On the CPU torch keeps the fp32 divisor for a
+    reduced-precision tensor, so the divisor is rounded here explicitly."""
+    x = _typed_inputs()
+    for dtype, tdt in (("f16", torch.float16), ("f32", torch.float32)):
+        xt = x.to(tdt)
+        bits = xt.view(torch.int16).numpy().view(np.uint16) if dtype == "f16" else xt.numpy()
+        q, s = oracle.quant_tensor_e4m3_typed(bits, dtype, True, static)
+        amax = np.float32(xt.abs().max().float().item())
+        expect_s = np.float32(static) if static is not None else max(amax * (np.float32(1.0) / np.float32(448.0)),
+                                                                      np.float32(1e-12))
+        assert s == expect_s
+        d = torch.tensor(float(s), dtype=torch.float32).to(tdt).float()
+        ref = torch.clamp((xt.float() / d).to(tdt), -448.0, 448.0).to(torch.float8_e4m3fn)
+        np.testing.assert_array_equal(q, bits8(ref))
+        # Triton form: fp32 divisor, quotient rounded to bf16, for any input dtype
+        qt, _ = oracle.quant_tensor_e4m3_typed(bits, dtype, False, static)
+        ref_t = torch.clamp((xt.float() / torch.tensor(float(s))).to(torch.bfloat16), -448.0, 448.0)
+        np.testing.assert_array_equal(qt, bits8(ref_t.to(torch.float8_e4m3fn)))
+        if dtype == "f16":
+            assert (q != qt).any()  # the two forms differ on this input
+
+
+def test_typed_tensor_quant_bf16_is_the_bf16_quantizer(oracle):
+    x = activations(48, 1024, seed=2, outlier_channels=5)
+    for eager in (False, True):
+        q, s = oracle.quant_tensor_e4m3_typed(bits16(x), "bf16", eager)
+        q0, s0 = oracle.quant_tensor_e4m3(bits16(x), bf16_divisor=eager)
+        np.testing.assert_array_equal(q, q0)
+        assert s == s0
+
+
+def test_typed_tensor_quant_zero_tensors(oracle):
+    """All zeros: the scale floors at 1e-12.  fp16(1e-12) is zero, so the
+    eager fp16 quotient is 0 / 0 = NaN and every code is the NaN 0x7F; fp32
+    divides by 1e-12 and gives zero codes; bf16(1e-12) is still positive."""
+    z16 = np.zeros((3, 16), np.uint16)
+    q, s = oracle.quant_tensor_e4m3_typed(z16, "f16", True)
+    assert s == np.float32(1e-12) and np.all(q == 0x7F)
+    ref = torch.clamp(torch.zeros(3, 16, dtype=torch.float16) / torch.tensor(1e-12).half(), -448, 448)
+    assert torch.isnan(ref).all()
+    q, _ = oracle.quant_tensor_e4m3_typed(np.zeros((3, 16), np.float32), "f32", True)
+    assert np.all(q == 0)
+    q, _ = oracle.quant_tensor_e4m3_typed(z16, "bf16", True)
+    assert np.all(q == 0)
+
+
+def test_f16_epilogue_rounds_once(oracle):
+    """out_f16: s_a * (s_w * acc) [+ fp16 bias as one FMA] rounded once to
+    binary16, against numpy (fp64 evaluation of the FMA, then fp32, then fp16)."""
+    rng = np.random.default_rng(9)
+    acc = rng.integers(-2 ** 20, 2 ** 20, size=(16, 24)).astype(np.int32)
+    sa = (rng.random(16) * 1e-3).astype(np.float32)
+    sw = (rng.random(24) * 1e-2).astype(np.float32)
+    bias = (rng.standard_normal(24) * 0.1).astype(np.float16)
+    t = sw[None, :] * acc.astype(np.float32)
+    plain = (sa[:, None] * t).astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(oracle.epilogue(acc, sa, sw, out_f16=True), plain)
+    fused = (sa[:, None].astype(np.float64) * t.astype(np.float64) + bias.astype(np.float64)[None, :])
+    ref = fused.astype(np.float32).astype(np.float16).view(np.uint16)
+    got = oracle.epilogue(acc, sa, sw, bias.view(np.uint16), out_f16=True)
+    np.testing.assert_array_equal(got, ref)
+    # a bf16 epilogue of the same values differs: the flag is honoured
+    assert (oracle.epilogue(acc, sa, sw) != plain).any()
