@@ -53,7 +53,7 @@ INT8_PEAK_TOPS = 5000.0    # MI355X dense INT8 MFMA
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 M, K, N = 8192, 5120, 15360
 TRAFFIC_FILE = ROOT / "profiles" / "gemm_fp8_c2_traffic.json"
-GEMM_KERNEL_TAG = "gemm_persistent_kernel<h3q::Tile<256, 256, 128, 2, 4, 4, 4>, 0, true, true>"
+GEMM_KERNEL_TAG = "gemm_w4_kernel<0, true, true, true, false>"
 
 
 def log(*a):
@@ -328,10 +328,10 @@ def bench_c5(torch, ops, dev) -> dict:
     y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
 
     def quant(_i):
-        ops.quant_rows(x, ops.FMT_INT8, ops.ROUND_RCP_MUL, codes=q_a, scales=s_a)
+        ops.quant_rows_tiled(x, ops.FMT_INT8, ops.ROUND_RCP_MUL, codes=q_a, scales=s_a)
 
     def gemm(_i):
-        ops.scaled_mm(q_a, qw, s_a.reshape(-1), sw.reshape(-1), out=y, b_tiled=True)
+        ops.scaled_mm(q_a, qw, s_a.reshape(-1), sw.reshape(-1), out=y, a_tiled=True, b_tiled=True, m=m)
 
     quant(0)
     gemm(0)
@@ -403,16 +403,23 @@ def main() -> int:
     xs, w, bias = make_inputs(torch, dev, rotations)
     q_w, s_w = ops.quant_rows_tiled(w, ops.FMT_E4M3FN)      # offline weight quantize + pack
     s_w = s_w.reshape(-1)
+    # Activation codes in the tiled layout (M is a multiple of 16), the
+    # operand layout the four-wave GEMM reads fastest.
     q_a = torch.empty(M, K, device=dev, dtype=torch.float8_e4m3fn)
     s_a = torch.empty(M, 1, device=dev, dtype=torch.float32)
     out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
     torch.cuda.synchronize()
 
     def quant(i: int):
-        ops.quant_rows(xs[i % rotations], ops.FMT_E4M3FN, codes=q_a, scales=s_a)
+        ops.quant_rows_tiled(xs[i % rotations], ops.FMT_E4M3FN, codes=q_a, scales=s_a)
 
     def gemm(_i: int):
-        ops.scaled_mm(q_a, q_w, s_a.reshape(-1), s_w, bias=bias, out=out, b_tiled=True)
+        ops.scaled_mm(q_a, q_w, s_a.reshape(-1), s_w, bias=bias, out=out, a_tiled=True, b_tiled=True, m=M)
+
+    def quant_row_major(i: int):
+        ops.quant_rows(xs[i % rotations], ops.FMT_E4M3FN, codes=q_rm, scales=s_a)
+
+    q_rm = torch.empty(M, K, device=dev, dtype=torch.float8_e4m3fn)
 
     def step(i: int, ev=None):
         if ev is not None:
@@ -470,6 +477,7 @@ def main() -> int:
     q_step_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
     g_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
     q_ms = time_events(torch, quant, 4 * rotations)        # act-quant back to back, rotating inputs
+    q_rm_ms = time_events(torch, quant_row_major, 4 * rotations)
 
     flops = 2.0 * M * N * K
     ms_per_step = elapsed / args.steps * 1e3
@@ -503,7 +511,7 @@ def main() -> int:
         "config": {
             "workload": "c2: DiT QKV projection, 480p streaming chunk (BASELINE configs[1])",
             "M_tokens": M, "K": K, "N": N,
-            "act_quant": "per-token dynamic e4m3fn",
+            "act_quant": "per-token dynamic e4m3fn, codes in the tiled layout",
             "weight_quant": "per-output-channel e4m3fn (offline, tiled layout)",
             "bias": True, "out": "bf16",
             "activation_buffers_rotated": rotations,
@@ -512,7 +520,7 @@ def main() -> int:
         "eager_ms_per_step": round(eager_elapsed / args.steps * 1e3, 4),
         "pct_fp8_peak": round(100.0 * value / FP8_PEAK_TFLOPS, 2),
         "roofline": {
-            "kernel": "h3q gemm_persistent_kernel (scaled e4m3 GEMM + dequant + bias epilogue)",
+            "kernel": "h3q gemm_w4_kernel (four-wave persistent scaled e4m3 GEMM + dequant + bias epilogue)",
             "bound": "mfma",
             "achieved": round(gemm_tflops, 2),
             "peak": FP8_PEAK_TFLOPS,
@@ -523,7 +531,7 @@ def main() -> int:
             "algorithmic_flops": flops,
         },
         "act_quant": {
-            "kernel": "h3q quant_rows_vec_kernel (per-token e4m3fn)",
+            "kernel": "h3q quant_rows_tiled_block_kernel (per-token e4m3fn, tiled codes)",
             "bound": "hbm",
             "achieved": round(q_gbs, 1),
             "peak": HBM_PEAK_GBS,
@@ -532,6 +540,9 @@ def main() -> int:
             "avg_launch_us": round(q_ms * 1e3, 2),
             "in_step_us": round(q_step_ms * 1e3, 2),
             "algorithmic_bytes": q_bytes,
+            "row_major_kernel": "h3q quant_rows_vec_kernel",
+            "row_major_us": round(q_rm_ms * 1e3, 2),
+            "row_major_frac": round(q_bytes / (q_rm_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         },
     }
     if args.calibrate_copy:
@@ -543,7 +554,7 @@ def main() -> int:
         result["calibration_copy_bytes"] = int(src.numel() * src.element_size())
         del src, dst
     x_cpu, w_cpu, bias_cpu = xs[0].cpu(), w.cpu(), bias.cpu()
-    del xs, w, q_w, q_a, out
+    del xs, w, q_w, q_a, q_rm, out
     torch.cuda.empty_cache()
     if not args.no_extra:
         log("secondary configs: c3, c4, c5, f1, f4, a6")

@@ -26,7 +26,7 @@ LAYOUT_TILED = 1
 OUT_F16 = 0x100      # scaled_mm format flag: binary16 output and bias
 QUOTIENT_EAGER = 0   # per-tensor quotient forms of h3q_quant_tensor_e4m3_typed
 QUOTIENT_TRITON = 1
-SKINNY_MAX_M = 128   # tiled activations (weight-streaming GEMM) up to this many rows
+SKINNY_MAX_M = 128   # rows up to which the weight-streaming GEMM runs
 
 _CODE_DTYPES = {FMT_E4M3FN: torch.float8_e4m3fn, FMT_INT8: torch.int8}
 _FORMATS = {torch.float8_e4m3fn: FMT_E4M3FN, torch.int8: FMT_INT8}
@@ -221,12 +221,16 @@ def check_layout(name: str, t: torch.Tensor, tiled: bool) -> None:
 def quant_activations_for(x: torch.Tensor, fmt: int, rounding: int, weight: torch.Tensor, *,
                           codes: torch.Tensor | None = None, scales: torch.Tensor | None = None):
     """Per-token quantization of the 2-D activations of a linear whose weight
-    codes are ``weight``: tiled (for the weight-streaming GEMM) when the
-    weight is tiled and there are at most 128 tokens, else row-major.
-    Returns (codes, scales, a_tiled); ``codes`` may be a larger workspace
-    buffer of rows >= tiled_rows(m)."""
+    codes are ``weight`` (bf16 output, no LoRA): tiled when the weight is
+    tiled and the GEMM reads tiled activations at this shape -- the
+    weight-streaming GEMM for at most 128 tokens, the four-wave GEMM above
+    that (K >= 256, N a multiple of 8) -- else row-major.  Returns (codes,
+    scales, a_tiled); ``codes`` may be a larger workspace buffer of rows >=
+    tiled_rows(m)."""
     m, k = x.shape
-    if is_tiled(weight) and 0 < m <= SKINNY_MAX_M and k % 128 == 0:
+    n = int(weight.shape[0])
+    fits = 0 < m <= SKINNY_MAX_M or (m > SKINNY_MAX_M and k >= 256 and n % 8 == 0)
+    if is_tiled(weight) and k % 128 == 0 and fits:
         buf = None if codes is None else codes[:tiled_rows(m)]
         q, s = quant_rows_tiled(x, fmt, rounding, codes=buf, scales=scales)
         return q, s, True

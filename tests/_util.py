@@ -62,3 +62,9 @@ def to_tiled(codes: np.ndarray) -> np.ndarray:
     r, k = codes.shape
     c = np.ascontiguousarray(codes).reshape(r // 16, 16, k // 128, 4, 2, 16)  # b, r16, s, q, h, byte
     return np.ascontiguousarray(c.transpose(0, 2, 4, 3, 1, 5)).reshape(r, k)  # b, s, h, q, r16, byte
+
+
+def from_tiled(tiled: np.ndarray, r: int, k: int) -> np.ndarray:
+    """Inverse of to_tiled: the tiled bytes of an [R, K] code matrix -> row-major [R, K]."""
+    t = np.ascontiguousarray(tiled).reshape(r // 16, k // 128, 2, 4, 16, 16)  # b, s, h, q, r16, byte
+    return np.ascontiguousarray(t.transpose(0, 4, 1, 3, 2, 5)).reshape(r, k)

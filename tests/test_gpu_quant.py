@@ -154,7 +154,8 @@ def test_full_size_activations(ops, oracle, device, name, m, k, fmt, rounding, s
 
 
 @pytest.mark.parametrize("fmt,rounding", [("e4m3", "div"), ("int8", "div"), ("int8", "rcp")])
-@pytest.mark.parametrize("n,k,chunk", [(64, 512, 64), (96, 1024, 40), (48, 5120, 7), (16, 128, 16)])
+@pytest.mark.parametrize("n,k,chunk", [(64, 512, 64), (96, 1024, 40), (48, 5120, 7), (16, 128, 16),
+                                       (80, 5376, 48), (32, 13824, 32), (64, 7168, 50)])
 def test_tiled_quantizer_matches_permuted_oracle(ops, oracle, device, fmt, rounding, n, k, chunk):
     """h3q_quant_rows_tiled in row chunks (any chunk size, like the streamed
     loader) == the oracle's row-major codes permuted into the tiled layout."""
@@ -173,6 +174,25 @@ def test_tiled_quantizer_matches_permuted_oracle(ops, oracle, device, fmt, round
     rq, rs = oracle.quant_rows(bits16(w), fmt, rounding)
     np.testing.assert_array_equal(bits8(codes), to_tiled(rq.view(np.uint8)))
     np.testing.assert_array_equal(scales.cpu().numpy().ravel(), rs)
+
+
+@pytest.mark.parametrize("m,k,fmt,rounding", [(8192, 5120, "e4m3", "div"), (4100, 13824, "e4m3", "div"),
+                                               (2064, 5120, "int8", "rcp")])
+def test_tiled_activations_full_size(ops, oracle, device, m, k, fmt, rounding):
+    """Activation codes written straight into the tiled layout by whole
+    16-row blocks (plus a ragged tail), at the c2 / c3-down / c5 widths."""
+    from _util import from_tiled
+
+    print(f"tiled act quant {m}x{k} {fmt}", flush=True)
+    x = activations(m, k, seed=m, outlier_channels=max(1, k // 100), outlier_scale=15.0)
+    f = ops.FMT_E4M3FN if fmt == "e4m3" else ops.FMT_INT8
+    r = ops.ROUND_DIV if rounding == "div" else ops.ROUND_RCP_MUL
+    q, s = ops.quant_rows_tiled(x.to(device), f, r)
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_rows(bits16(x), fmt, rounding)
+    # rows past m are padding of the last block: compare the real rows
+    np.testing.assert_array_equal(from_tiled(bits8(q), q.shape[0], k)[:m], rq.view(np.uint8))
+    np.testing.assert_array_equal(s.cpu().numpy().ravel(), rs)
 
 
 def test_int8_rcp_known_answers(ops, device):
