@@ -11,6 +11,7 @@ from __future__ import annotations
 import os
 import shutil
 import subprocess
+from concurrent.futures import ThreadPoolExecutor
 import sys
 from pathlib import Path
 
@@ -42,20 +43,26 @@ def _quiet(text: str) -> str:
     return "\n".join(l for l in text.splitlines() if "packed-fp32-ops" not in l)
 
 
+def _compile(cc: str, src: str, obj: Path) -> subprocess.CompletedProcess:
+    cmd = [cc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    return subprocess.run(cmd, capture_output=True, text=True)
+
+
 def build(verbose: bool = False) -> Path:
     objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
-    objects = []
     cc = hipcc()
-    for src in SOURCES:
-        obj = objdir / (src + ".o")
-        cmd = [cc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
-        res = subprocess.run(cmd, capture_output=True, text=True)
+    objects = [objdir / (src + ".o") for src in SOURCES]
+    # One hipcc per source, at most as many at once as there are CPUs (8 here).
+    workers = max(1, min(len(SOURCES), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        results = list(pool.map(lambda so: _compile(cc, *so), zip(SOURCES, objects)))
+    for src, res in zip(SOURCES, results):
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed on {src}:\n{_quiet(res.stderr)}")
         if verbose and _quiet(res.stderr).strip():
             print(_quiet(res.stderr), file=sys.stderr)
-        objects.append(str(obj))
+    objects = [str(o) for o in objects]
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [cc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *objects]
     res = subprocess.run(cmd, capture_output=True, text=True)
