@@ -54,6 +54,8 @@
 // the same k order.
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "gemm_tiles.hpp"
 #include "h3q_common.hpp"
 #include "h3q_kernels.hpp"
@@ -123,13 +125,21 @@ struct W4Op<kOpInt8> {
 
 // F16: binary16 output and bias instead of bf16 (a separate instance, so the
 // bf16 epilogue carries no select).
+//
+// Schedule.  Workgroup b takes tiles b, b + G, ... (G = gridDim.x).  When the
+// last round of tiles is at most half full (0 < T % G <= G / 2 for T tiles)
+// and split_tail is set, that round's tiles are cut into two 128 x 256 halves
+// instead, and every workgroup b < 2 (T % G) finishes with one half (tile
+// rounds * G + b % (T % G), rows 128 * (b / (T % G)) ..): the last round then
+// keeps every CU busy for about half a round instead of leaving half the CUs
+// idle for a full one.  A half tile runs the same ring and k order with two
+// 32-row blocks per wave (waves 2 x 2 of 64 x 128), so its outputs carry the
+// same bits as in a whole tile.
 template <int OP, bool BIAS, bool TA, bool TB, bool F16>
-__global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m, int tiles_n) {
+__global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m, int tiles_n, int split_tail) {
     using acc_t = typename W4Op<OP>::acc_t;
     using frag_t = typename W4Op<OP>::frag_t;
     constexpr int KS = W4Op<OP>::kSteps;
-    constexpr int NM = 16 * KS;                   // MFMAs per step per wave
-    constexpr int NR = OP == kOpE4M3 ? 8 : 16;    // fragment reads (of 1 or 2 ds_read_b128) per step
     __shared__ __attribute__((aligned(1024))) uint8_t lds_ring[kW4Stages * kW4StageBytes];
     // Per tile parity: row scales [256] f32 | column scales [256] f32 | bias [256] bf16.
     __shared__ __attribute__((aligned(1024))) uint8_t lds_ep[2 * 3 * 1024];
@@ -139,11 +149,26 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm0 = (wave >> 1) * 128, wn0 = (wave & 1) * 128;
+    const int wn0 = (wave & 1) * 128;
     const int g = lane >> 5, c32 = lane & 31;
     const int ksteps = (int)(p.k / 64);          // even: k % 128 == 0
     const int64_t steps128 = p.k / 128;          // tiled operands: 128-byte k-steps per block row
-    const int ntiles = (tiles_m * tiles_n - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+
+    // Work items j < nfull are whole tiles; item nfull (has_half) is a half tile.
+    const int T = tiles_m * tiles_n, G = (int)gridDim.x, b = (int)blockIdx.x;
+    const int rounds = T / G, rem = T % G;
+    const bool split = split_tail != 0 && rem > 0 && 2 * rem <= G;
+    const int nfull = split ? rounds : (T - b + G - 1) / G;
+    int half_tm = 0, half_tn = 0, half_m0 = 0;
+    bool has_half = false;
+    if (split && b < 2 * rem) {
+        tile_coords(rounds * G + b % rem, tiles_m, tiles_n, half_tm, half_tn);
+        half_m0 = half_tm * 256 + 128 * (b / rem);
+        has_half = p.m > half_m0;
+    }
+    const int ntiles = nfull + (has_half ? 1 : 0);
+    if (ntiles == 0) return;
+
     const bool row_scales = p.a_scale_per_row != 0, col_scales = p.b_scale_per_col != 0;
     // A per-tensor scale fills its vector (both parities) once.
     if (!row_scales || !col_scales) {
@@ -155,16 +180,25 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         }
     }
 
+    // Every lambda below is force-inlined: an outlined one would take its
+    // captures through private memory, and the copy instructions' scalar
+    // operands (descriptors, LDS bases, offsets) would stop being uniform.
     struct TileSrc {
         int m0, n0, rows, cols;
     };
-    auto tile_src = [&](int j) {
-        int tm, tn;
-        tile_coords((int)blockIdx.x + j * (int)gridDim.x, tiles_m, tiles_n, tm, tn);
+    auto tile_src = [&](int j) __attribute__((always_inline)) {
         TileSrc t;
-        t.m0 = tm * 256;
+        int tm, tn;
+        if (j < nfull) {
+            tile_coords(b + j * G, tiles_m, tiles_n, tm, tn);
+            t.m0 = tm * 256;
+        } else {
+            tn = half_tn;
+            t.m0 = half_m0;
+        }
+        const int mrows = j < nfull ? 256 : 128;
         t.n0 = tn * 256;
-        t.rows = (int)(p.m - t.m0 < 256 ? p.m - t.m0 : 256);
+        t.rows = (int)(p.m - t.m0 < mrows ? p.m - t.m0 : mrows);
         t.cols = (int)(p.n - t.n0 < 256 ? p.n - t.n0 : 256);
         return t;
     };
@@ -172,11 +206,12 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     // ---------------------------------------------------------------- copies
     // Descriptors and per-lane offsets of the tile being fetched; the k-step
     // enters as the scalar offset.  Past the last tile the descriptors are
-    // empty, so the trailing copies read zeros into stages nobody reads.
+    // empty, so the trailing copies read zeros into stages nobody reads.  A
+    // half tile's A rows past 128 are out of range too (zeros, never read).
     CopySrc ra(nullptr, 0), rb(nullptr, 0);
     uint32_t voff_a[4], voff_b[4];
     int cj = 0, cs = 0;  // tile / k-step of the next copy group
-    auto operand_offset = [&](bool tiled, int c, int sub_row, int pos, int ln, int rows, int64_t ld) -> uint32_t {
+    auto operand_offset = [&](bool tiled, int c, int sub_row, int pos, int ln, int rows, int64_t ld) __attribute__((always_inline)) -> uint32_t {
         if (tiled) {  // 16-row block c
             const int nblk = (rows + 15) / 16;
             return c < nblk ? (uint32_t)(c * steps128 * 2048) + (uint32_t)((ln >> 5) * 1024 + (ln & 31) * 16)
@@ -185,7 +220,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         const int row = c * 16 + sub_row;  // 16 rows x 64 bytes per copy
         return row < rows ? (uint32_t)row * (uint32_t)ld + (uint32_t)((pos ^ swz64(sub_row)) * 16) : 0x80000000u;
     };
-    auto setup_copy_tile = [&](int j) {
+    auto setup_copy_tile = [&](int j) __attribute__((always_inline)) {
         const bool live = j < ntiles;
         const TileSrc t = tile_src(live ? j : ntiles - 1);
         const uint32_t a_bytes = TA ? (uint32_t)((t.rows + 15) / 16 * steps128 * 2048) : (uint32_t)((int64_t)t.rows * p.lda);
@@ -203,7 +238,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         }
     };
     // Epilogue vectors of tile j into LDS (waves 0, 1, 2: one copy each).
-    auto issue_vectors = [&](int j) {
+    auto issue_vectors = [&](int j) __attribute__((always_inline)) {
         if (j >= ntiles) return;
         const TileSrc t = tile_src(j);
         H3Q_LDS uint8_t* e = ep + (j & 1) * 3072;
@@ -216,7 +251,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
                    lane < 32 ? 16u * lane : 0x80000000u);
     };
     // Copy q (0..3: A, 4..7: B) of the group for (cj, cs) into stage st.
-    auto issue_copy = [&](int q, int st) {
+    auto issue_copy = [&](int q, int st) __attribute__((always_inline)) {
         const uint32_t base = ring_addr + (uint32_t)(st * kW4StageBytes);
         const uint32_t soff_t = (uint32_t)((cs >> 1) * 2048 + (cs & 1) * 512), soff_r = (uint32_t)(cs * 64);
         if (q < 4)
@@ -225,7 +260,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
             copy16_soff(rb, base + (uint32_t)(kW4ABytes + (wave + 4 * (q - 4)) * 1024), voff_b[q - 4],
                         TB ? soff_t : soff_r);
     };
-    auto advance_copy = [&]() {
+    auto advance_copy = [&]() __attribute__((always_inline)) {
         if (++cs == ksteps) {
             cs = 0;
             ++cj;
@@ -239,34 +274,48 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     // wm0 + c32 (A) and wn0 + c32 (B) of the first 32-row block; block i adds
     // 2048 in either layout.  e4m3: halves h = 0, 1 of the 32-byte fragment
     // (k bytes 32 g + 16 h); int8: k-steps s = 0, 1 (k bytes 32 s + 16 g).
-    uint32_t rda[2], rdb[2];
+    // A whole tile puts a wave's rows at wm0 = 128 (wave / 2), a half tile at
+    // 64 (wave / 2); rda holds the offsets of the layout being read.
+    uint32_t rda[2], rda_half[2], rdb[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int chunk = OP == kOpE4M3 ? 2 * g + h : 2 * h + g;      // logical 16-byte chunk of the row
         const int tiled_off = ((c32 & 15) + 16 * (OP == kOpE4M3 ? g : h)) * 16 + (OP == kOpE4M3 ? h : g) * 512;
-        rda[h] = TA ? (uint32_t)(((wm0 + c32) >> 4) * 1024 + tiled_off)
-                    : (uint32_t)((wm0 + c32) * 64 + ((chunk ^ swz64(c32)) << 4));
+        auto a_off = [&](int wm0) __attribute__((always_inline)) {
+            return TA ? (uint32_t)(((wm0 + c32) >> 4) * 1024 + tiled_off)
+                      : (uint32_t)((wm0 + c32) * 64 + ((chunk ^ swz64(c32)) << 4));
+        };
+        rda[h] = a_off((wave >> 1) * 128);
+        rda_half[h] = a_off((wave >> 1) * 64);
         rdb[h] = kW4ABytes + (TB ? (uint32_t)(((wn0 + c32) >> 4) * 1024 + tiled_off)
                                  : (uint32_t)((wn0 + c32) * 64 + ((chunk ^ swz64(c32)) << 4)));
     }
+    auto to_half_layout = [&]() __attribute__((always_inline)) {
+        rda[0] = rda_half[0];
+        rda[1] = rda_half[1];
+    };
     struct Frags {
         frag_t a[4 * KS], b[4 * KS];
     };
-    auto ld16 = [&](const H3Q_LDS uint8_t* ptr) -> v4i { return *(const H3Q_LDS v4i*)ptr; };
-    // Fragment x of stage st (e4m3: a0..a3, b0..b3; int8: a[i + 4 s], b[i + 4 s]).
-    auto read_frag = [&](Frags& F, int x, int st) {
+    auto ld16 = [&](const H3Q_LDS uint8_t* ptr) __attribute__((always_inline)) -> v4i { return *(const H3Q_LDS v4i*)ptr; };
+    // Fragment x of stage st for MI 32-row A blocks per wave: x < MI * KS
+    // reads A block x % MI (k-step x / MI), the rest B block (x - MI KS) % 4
+    // (k-step (x - MI KS) / 4).
+    auto read_frag = [&](auto mi, Frags& F, int x, int st) __attribute__((always_inline)) {
+        constexpr int MI = decltype(mi)::value;
         const H3Q_LDS uint8_t* sb = ring + st * kW4StageBytes;
+        const bool is_a = x < MI * KS;
+        const int xx = is_a ? x : x - MI * KS;
+        const int y = is_a ? xx % MI : xx % 4, s = is_a ? xx / MI : xx / 4;
         if constexpr (OP == kOpE4M3) {
-            const int y = x & 3;
-            const uint32_t* off = x < 4 ? rda : rdb;
+            const uint32_t* off = is_a ? rda : rdb;
             const v8i f = __builtin_shufflevector(ld16(sb + off[0] + y * 2048), ld16(sb + off[1] + y * 2048), 0, 1, 2,
                                                   3, 4, 5, 6, 7);
-            if (x < 4) F.a[y] = f;
+            if (is_a) F.a[y] = f;
             else F.b[y] = f;
         } else {
-            const int y = x & 3, s = (x & 7) >> 2;
-            const v4i f = ld16(sb + (x < 8 ? rda[s] : rdb[s]) + y * 2048);
-            if (x < 8) F.a[y + 4 * s] = f;
+            const v4i f = ld16(sb + (is_a ? rda[s] : rdb[s]) + y * 2048);
+            if (is_a) F.a[y + 4 * s] = f;
             else F.b[y + 4 * s] = f;
         }
     };
@@ -274,8 +323,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     acc_t acc[4][4];
     Frags F0, F1;
     // MFMA t of a step: acc[i][j] += b-fragment j x a-fragment i (k-step s).
-    auto mfma = [&](bool first, const Frags& Fc, int t) {
-        const int s = t / 16, i = (t % 16) / 4, j = t % 4;
+    auto mfma = [&](auto mi, bool first, const Frags& Fc, int t) __attribute__((always_inline)) {
+        constexpr int MI = decltype(mi)::value;
+        const int s = t / (4 * MI), i = (t % (4 * MI)) / 4, j = t % 4;
         if constexpr (OP == kOpE4M3) {
             if (first) mfma_e4m3_first(acc[i][j], Fc.b[j], Fc.a[i]);
             else mfma_e4m3(acc[i][j], Fc.b[j], Fc.a[i]);
@@ -286,19 +336,27 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     };
     // One step's instruction stream: every MFMA is followed by the next
     // fragment read (first NR slots) or copy (next 8 slots), each slot kept
-    // in place by a scheduling barrier.
-    auto body = [&](bool first, const Frags& Fc, Frags& Fn, int rst, int cst) {
+    // in place by a scheduling barrier.  The reads of the next stage use the
+    // layout of MI = 4 (a superset of a half tile's: the extra A blocks are
+    // read and never used), so a step may prepare a half tile's first step.
+    auto body = [&](auto mi, bool first, const Frags& Fc, Frags& Fn, int rst, int cst) __attribute__((always_inline)) {
+        constexpr int MI = decltype(mi)::value;
+        constexpr int NM = 4 * MI * KS;                  // MFMAs per step per wave
+        constexpr int NR = (4 + 4) * KS;                 // fragment reads per step
+        constexpr int NT = NM > NR + 8 ? NM : NR + 8;
 #pragma unroll
-        for (int t = 0; t < NM; ++t) {
-            mfma(first, Fc, t);
-            if (t < NR) read_frag(Fn, t, rst);
+        for (int t = 0; t < NT; ++t) {
+            if (t < NM) mfma(mi, first, Fc, t);
+            if (t < NR) read_frag(std::integral_constant<int, 4>(), Fn, t, rst);
             else if (t - NR < 8) issue_copy(t - NR, cst);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
     // ------------------------------------------------------------- epilogue
-    auto epilogue = [&](int mj, int st) {
+    auto epilogue = [&](auto mi, int mj, int st) __attribute__((always_inline)) {
+        constexpr int MI = decltype(mi)::value;
+        const int wm0 = (wave >> 1) * 32 * MI;
         const TileSrc cur = tile_src(mj);
         const int ln = opaque_lane();
         const int gg = ln >> 5, cc = ln & 31;
@@ -309,9 +367,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         // This lane's vectors, read once (before any scratch write): row
         // scales of rows wm0 + 32 i + cc; column scales and bias of columns
         // wn0 + 8 g16 + 4 gg + x, g16 = 4 jj + q.
-        float sa[4];
+        float sa[MI];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sa[i] = ((const H3Q_LDS float*)e)[wm0 + 32 * i + cc];
+        for (int i = 0; i < MI; ++i) sa[i] = ((const H3Q_LDS float*)e)[wm0 + 32 * i + cc];
         v4f sw4[16];
         v2u b4[16];
 #pragma unroll
@@ -326,7 +384,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         // VALU reads of MFMA results: wait out the last MFMAs' passes.
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < MI; ++i) {
 #pragma unroll
             for (int g16 = 0; g16 < 16; ++g16) {
                 const int jj = g16 >> 2, q = g16 & 3;
@@ -366,33 +424,41 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         for (int q = 0; q < 8; ++q) issue_copy(q, st);
         advance_copy();
     }
+    if (nfull == 0) to_half_layout();
     wait_vmcnt<(kW4Stages - 1) * 8>();
     ring_barrier();
 #pragma unroll
-    for (int x = 0; x < NR; ++x) read_frag(F0, x, 0);
+    for (int x = 0; x < 8 * KS; ++x) read_frag(std::integral_constant<int, 4>(), F0, x, 0);
     wait_vmcnt<(kW4Stages - 2) * 8>();
     ring_barrier();
 
     int cur_st = 0;  // stage of the running step (its fragments are in registers)
-    auto step = [&](bool first, const Frags& Fc, Frags& Fn) {
+    auto step = [&](auto mi, bool first, const Frags& Fc, Frags& Fn) __attribute__((always_inline)) {
         const int nxt_st = cur_st + 1 == kW4Stages ? 0 : cur_st + 1;
-        body(first, Fc, Fn, nxt_st, cur_st);
+        body(mi, first, Fc, Fn, nxt_st, cur_st);
         advance_copy();
         wait_vmcnt<(kW4Stages - 2) * 8>();
         ring_barrier();
         cur_st = nxt_st;
     };
-    for (int mj = 0; mj < ntiles; ++mj) {
-        step(true, F0, F1);
-        step(false, F1, F0);
+    // One tile: ksteps steps (the last one reads the next tile's first
+    // fragments, in the half layout when a half tile follows), then the
+    // epilogue through the stage that is free until the next step's copies.
+    auto run_tile = [&](auto mi, int mj, bool next_half) __attribute__((always_inline)) {
+        const std::integral_constant<int, decltype(mi)::value> m;
+        step(m, true, F0, F1);
+        if (ksteps == 2 && next_half) to_half_layout();
+        step(m, false, F1, F0);
         for (int s = 2; s < ksteps; s += 2) {
-            step(false, F0, F1);
-            step(false, F1, F0);
+            step(m, false, F0, F1);
+            if (s + 2 == ksteps && next_half) to_half_layout();
+            step(m, false, F1, F0);
         }
-        // Stage cur_st is free until the next step's copies: stage through it.
-        epilogue(mj, cur_st);
+        epilogue(m, mj, cur_st);
         ring_barrier();
-    }
+    };
+    for (int mj = 0; mj < nfull; ++mj) run_tile(std::integral_constant<int, 4>(), mj, has_half && mj + 1 == nfull);
+    if (has_half) run_tile(std::integral_constant<int, 2>(), nfull, false);
     wait_vmcnt<0>();
 }
 
@@ -414,14 +480,14 @@ static hipError_t launch_w4_op(const GemmArgs& a, hipStream_t st) {
     const int tiles_m = (int)((a.m + 255) / 256), tiles_n = (int)((a.n + 255) / 256);
     const dim3 grid((unsigned)persistent_grid(tiles_m * tiles_n));
     if (a.out_f16) {
-        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, true, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
-        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, false, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, true, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
+        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, false, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
     } else if (a.a_tiled) {
-        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, true, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
-        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, false, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, true, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
+        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, false, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
     } else {
-        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, true, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
-        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, false, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n);
+        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, true, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
+        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, false, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
     }
     return hipGetLastError();
 }

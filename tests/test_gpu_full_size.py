@@ -231,3 +231,32 @@ def test_ragged_large_m_tiled_activations(ops, oracle, device):
     rqa, rsa = oracle.quant_rows(bits16(x), "int8", "rcp")
     rqw, rsw = oracle.quant_rows(bits16(w), "int8", "div")
     np.testing.assert_array_equal(bits16(out), oracle.epilogue(oracle.gemm_i8_i32(rqa, rqw), rsa, rsw))
+
+
+@pytest.mark.parametrize("fmt", ["int8", "e4m3"])
+def test_split_tail_ragged_half_tiles(ops, oracle, device, fmt):
+    """300 tile-rows of one tile-column (m = 299 * 256 + 100, n = 200, k = 256,
+    bias, tiled weights): on a 256-workgroup grid the last round holds 44
+    tiles, so they run as 128-row halves, the ragged last tile-row among them
+    (its second half is empty).  int8: every output bit-exact.  e4m3: the
+    first tile-row and the last 1380 rows against the instruction model."""
+    m, n, k = 299 * 256 + 100, 200, 256
+    f = ops.FMT_E4M3FN if fmt == "e4m3" else ops.FMT_INT8
+    ar = ops.ROUND_DIV if fmt == "e4m3" else ops.ROUND_RCP_MUL
+    print(f"split tail {fmt}: {m}x{n}x{k}", flush=True)
+    x = activations(m, k, seed=21, outlier_channels=3, outlier_scale=15.0)
+    w = weights(n, k, seed=22)
+    bias = _bias(n, 23)
+    qw, sw = _quant_weights(ops, w, device, fmt)
+    qa, sa = ops.quant_rows(x.to(device), f, ar)
+    out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), bias=bias.to(device), b_tiled=True, n=n)
+    torch.cuda.synchronize()
+    rqw, rsw = oracle.quant_rows(bits16(w), fmt, "div")
+    if fmt == "int8":
+        rqa, rsa = oracle.quant_rows(bits16(x), "int8", "rcp")
+        ref = oracle.epilogue(oracle.gemm_i8_i32(rqa, rqw), rsa, rsw, bits16(bias))
+        np.testing.assert_array_equal(bits16(out), ref)
+    else:
+        rows = np.concatenate([np.arange(0, 256), np.arange(m - 1380, m)])
+        rqa, rsa = oracle.quant_rows(bits16(x[torch.from_numpy(rows)]), "e4m3")
+        _assert_fp8_close(oracle, bits16(out)[rows], rqa, rsa, rqw, rsw, bits16(bias))
