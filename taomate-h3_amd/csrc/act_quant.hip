@@ -178,6 +178,93 @@ __global__ __launch_bounds__(ROWS * 64) void quant_rows_tiled_block_kernel(const
     }
 }
 
+// Tiled output by half blocks through a whole-row LDS image (K % 128 == 0,
+// row0 % 16 == 0, K <= 16384).  A workgroup of 8 waves owns 8 rows (half of a
+// 16-row block), one row per wave held in VGPRs as in the row kernel above.
+// The codes of all 8 rows are written into an LDS image of 8 x K bytes, then
+// read back in the order of the tiled layout and stored as 16-byte pieces:
+// inside the 2 KiB tile of k-step s, the half block's rows fill four 128-byte
+// runs per 1 KiB half (rows 8 * half + r of fragment group q at slot
+// 8 * half + r + 16 q), so 64 consecutive threads store 8 whole 128-byte
+// lines.  Two barriers per unit: one before the read-back, one before the
+// image is written again.
+//
+// Image: row r at r * W, W = K rounded up to 256 bytes; its 16-byte chunk c
+// (codes 16 c .. 16 c + 15) sits at chunk (c & ~15) | ((c & 15) ^ g(r)),
+// g(r) = (r & 1) | (r >> 1) << 2, which stays inside the row's W bytes.
+// A wave's 8-byte writes (one row, consecutive chunks) stay a permutation of
+// 256-byte groups, and the read-back of 16 consecutive slots (rows 0..7 of
+// two fragment groups q, q + 1, chunks c and c ^ 2) hits 16 distinct 16-byte
+// bank groups.  Each workgroup walks units u, u + grid, ...; the next unit's
+// rows are loaded into a second register set before the read-back, so reads
+// of X overlap the stores.
+__device__ __forceinline__ int img_chunk(int c, int r) { return (c & ~15) | ((c & 15) ^ ((r & 1) | ((r >> 1) << 2))); }
+
+template <int FMT, int ROUND, int NV, bool PREFETCH>
+__global__ __launch_bounds__(512) void quant_rows_tiled_img_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                   int64_t units, int k, uint8_t* __restrict__ q,
+                                                                   int64_t row0, float* __restrict__ scales) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t img[];
+    const int lane = threadIdx.x & 63;
+    const int r = threadIdx.x >> 6;  // row within the unit
+    const int nvec = k >> 3;
+    const int64_t steps = k >> 7;
+    const int w = (k + 255) & ~255;  // image row stride
+    uint4 v[NV], vn[PREFETCH ? NV : 1];
+    int64_t u = blockIdx.x;
+    if (u < units) load_row<NV>(x, ldx, 8 * u + r, nvec, lane, v);
+    while (u < units) {
+        const int64_t row = 8 * u + r;
+        uint32_t m = 0;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            m = pk_abs_max(m, v[i].x);
+            m = pk_abs_max(m, v[i].y);
+            m = pk_abs_max(m, v[i].z);
+            m = pk_abs_max(m, v[i].w);
+        }
+        const float amax = wave_max(amax_from_packed(m));
+        RowQuant<FMT, ROUND> rq;
+        rq.init(amax);
+        if (lane == 0) scales[row] = rq.s;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int vec = i * 64 + lane;  // codes 8 vec .. 8 vec + 7: chunk vec / 2, half vec % 2
+            if (vec < nvec) {
+                uint2 out;
+                out.x = rq.pack4(v[i].x, v[i].y);
+                out.y = rq.pack4(v[i].z, v[i].w);
+                *reinterpret_cast<uint2*>(img + r * w + img_chunk(vec >> 1, r) * 16 + (vec & 1) * 8) = out;
+            }
+        }
+        const int64_t un = u + gridDim.x;
+        if constexpr (PREFETCH) {
+            if (un < units) load_row<NV>(x, ldx, 8 * un + r, nvec, lane, vn);
+        }
+        __syncthreads();
+        // Read-back: slot t = ((s * 2 + h) * 4 + qq) * 8 + rr holds row rr,
+        // codes 128 s + 32 qq + 16 h .. + 15.
+        const int64_t blk = (row0 + 8 * u) >> 4;
+        const int half = (int)(((row0 + 8 * u) >> 3) & 1);
+        uint8_t* const qb = q + blk * steps * 2048;
+        const int slots = k >> 1;  // 8 rows x k bytes / 16
+        for (int t = threadIdx.x; t < slots; t += 512) {
+            const int rr = t & 7, qq = (t >> 3) & 3, h = (t >> 5) & 1, s = t >> 6;
+            const int c = 8 * s + 2 * qq + h;
+            const uint4 val = *reinterpret_cast<const uint4*>(img + rr * w + img_chunk(c, rr) * 16);
+            *reinterpret_cast<uint4*>(qb + (int64_t)s * 2048 + h * 1024 + (8 * half + rr + 16 * qq) * 16) = val;
+        }
+        __syncthreads();  // the image is written again by the next unit
+        if constexpr (PREFETCH) {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) v[i] = vn[i];
+        } else if (un < units) {
+            load_row<NV>(x, ldx, 8 * un + r, nvec, lane, v);
+        }
+        u = un;
+    }
+}
+
 // General path (any K, any alignment): one workgroup per row, two passes.
 template <int FMT, int ROUND, bool TILED>
 __global__ __launch_bounds__(256) void quant_rows_any_kernel(const uint16_t* __restrict__ x, int64_t ldx,
@@ -232,6 +319,33 @@ static hipError_t launch_rows_tiled_units(const uint16_t* x, int64_t ldx, int64_
 // Register budget of a lane: up to K = 6144 (NV <= 12) two rows fit in 128
 // VGPRs, so two workgroups share a CU; up to K = 14336 (NV <= 28) in 256,
 // one workgroup per CU; beyond that there is no prefetch.
+template <int FMT, int ROUND, int NV, bool PREFETCH>
+static hipError_t launch_rows_tiled_img_cfg(const uint16_t* x, int64_t ldx, int64_t blocks, int64_t k, uint8_t* q,
+                                            int64_t row0, float* scales, int per_cu, hipStream_t st) {
+    const int64_t units = blocks * 2;
+    const int64_t img_bytes = 8 * ((k + 255) & ~int64_t(255));
+    const int64_t cap = 256 * (int64_t)per_cu;
+    const int64_t grid = units < cap ? units : cap;
+    // Images above 64 KiB (K > 8192) need the kernel's dynamic LDS limit raised.
+    static const hipError_t lds_limit = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&quant_rows_tiled_img_kernel<FMT, ROUND, NV, PREFETCH>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, 8 * ((512 * NV + 255) & ~255));
+    if (lds_limit != hipSuccess) return lds_limit;
+    hipLaunchKernelGGL((quant_rows_tiled_img_kernel<FMT, ROUND, NV, PREFETCH>), dim3((unsigned)grid), dim3(512),
+                       (size_t)img_bytes, st, x, ldx, units, (int)k, q, row0, scales);
+    return hipGetLastError();
+}
+
+template <int FMT, int ROUND, int NV>
+static hipError_t launch_rows_tiled_img(const uint16_t* x, int64_t ldx, int64_t blocks, int64_t k, uint8_t* q,
+                                        int64_t row0, float* scales, hipStream_t st) {
+    // Workgroups of 8 waves: two per CU while the image (8 W bytes) and two
+    // row register sets per lane (128 VGPRs) fit twice, else one.
+    const int64_t img_bytes = 8 * ((k + 255) & ~int64_t(255));
+    const int per_cu = (NV <= 12 && img_bytes <= 80 * 1024) ? 2 : 1;
+    return launch_rows_tiled_img_cfg<FMT, ROUND, NV, true>(x, ldx, blocks, k, q, row0, scales, per_cu, st);
+}
+
 template <int FMT, int ROUND, int NV>
 static hipError_t launch_rows_tiled_block(const uint16_t* x, int64_t ldx, int64_t blocks, int64_t k, uint8_t* q,
                                           int64_t row0, float* scales, hipStream_t st) {
@@ -244,16 +358,16 @@ template <int FMT, int ROUND>
 static hipError_t dispatch_rows_tiled_block(const uint16_t* x, int64_t ldx, int64_t blocks, int64_t k, uint8_t* q,
                                             int64_t row0, float* scales, hipStream_t st) {
     const int64_t nv = (k + 511) / 512;
-    if (nv <= 2) return launch_rows_tiled_block<FMT, ROUND, 2>(x, ldx, blocks, k, q, row0, scales, st);
-    if (nv <= 4) return launch_rows_tiled_block<FMT, ROUND, 4>(x, ldx, blocks, k, q, row0, scales, st);
-    if (nv <= 8) return launch_rows_tiled_block<FMT, ROUND, 8>(x, ldx, blocks, k, q, row0, scales, st);
-    if (nv <= 10) return launch_rows_tiled_block<FMT, ROUND, 10>(x, ldx, blocks, k, q, row0, scales, st);
-    if (nv <= 11) return launch_rows_tiled_block<FMT, ROUND, 11>(x, ldx, blocks, k, q, row0, scales, st);
-    if (nv <= 14) return launch_rows_tiled_block<FMT, ROUND, 14>(x, ldx, blocks, k, q, row0, scales, st);
-    if (nv <= 16) return launch_rows_tiled_block<FMT, ROUND, 16>(x, ldx, blocks, k, q, row0, scales, st);
-    if (nv <= 24) return launch_rows_tiled_block<FMT, ROUND, 24>(x, ldx, blocks, k, q, row0, scales, st);
-    if (nv <= 28) return launch_rows_tiled_block<FMT, ROUND, 28>(x, ldx, blocks, k, q, row0, scales, st);
-    return launch_rows_tiled_block<FMT, ROUND, 32>(x, ldx, blocks, k, q, row0, scales, st);
+    if (nv <= 2) return launch_rows_tiled_img<FMT, ROUND, 2>(x, ldx, blocks, k, q, row0, scales, st);
+    if (nv <= 4) return launch_rows_tiled_img<FMT, ROUND, 4>(x, ldx, blocks, k, q, row0, scales, st);
+    if (nv <= 8) return launch_rows_tiled_img<FMT, ROUND, 8>(x, ldx, blocks, k, q, row0, scales, st);
+    if (nv <= 10) return launch_rows_tiled_img<FMT, ROUND, 10>(x, ldx, blocks, k, q, row0, scales, st);
+    if (nv <= 11) return launch_rows_tiled_img<FMT, ROUND, 11>(x, ldx, blocks, k, q, row0, scales, st);
+    if (nv <= 14) return launch_rows_tiled_img<FMT, ROUND, 14>(x, ldx, blocks, k, q, row0, scales, st);
+    if (nv <= 16) return launch_rows_tiled_img<FMT, ROUND, 16>(x, ldx, blocks, k, q, row0, scales, st);
+    if (nv <= 24) return launch_rows_tiled_img<FMT, ROUND, 24>(x, ldx, blocks, k, q, row0, scales, st);
+    if (nv <= 28) return launch_rows_tiled_img<FMT, ROUND, 28>(x, ldx, blocks, k, q, row0, scales, st);
+    return launch_rows_tiled_img<FMT, ROUND, 32>(x, ldx, blocks, k, q, row0, scales, st);
 }
 
 template <int FMT, int ROUND, bool TILED>

@@ -155,7 +155,8 @@ def test_full_size_activations(ops, oracle, device, name, m, k, fmt, rounding, s
 
 @pytest.mark.parametrize("fmt,rounding", [("e4m3", "div"), ("int8", "div"), ("int8", "rcp")])
 @pytest.mark.parametrize("n,k,chunk", [(64, 512, 64), (96, 1024, 40), (48, 5120, 7), (16, 128, 16),
-                                       (80, 5376, 48), (32, 13824, 32), (64, 7168, 50)])
+                                       (80, 5376, 48), (32, 13824, 32), (64, 7168, 50), (48, 640, 16),
+                                       (64, 16384, 32)])
 def test_tiled_quantizer_matches_permuted_oracle(ops, oracle, device, fmt, rounding, n, k, chunk):
     """h3q_quant_rows_tiled in row chunks (any chunk size, like the streamed
     loader) == the oracle's row-major codes permuted into the tiled layout."""
