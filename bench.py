@@ -90,8 +90,9 @@ def time_events(torch, fn, iters: int) -> float:
 
 def bench_c3(torch, ops, dev) -> dict:
     """FFN at 768p, M=24576, up N=13824 K=5120 and down
-    N=5120 K=13824, e4m3 per-token x per-channel, rank-128 LoRA (scale 1.0)
-    added in the GEMM epilogue.  Times act-quant + LoRA down + scaled GEMM."""
+    N=5120 K=13824, e4m3 per-token x per-channel (activation codes in the
+    tiled layout), rank-128 LoRA (scale 1.0) added in the GEMM epilogue.
+    Times act-quant + LoRA down + scaled GEMM."""
     gen = torch.Generator(device=dev).manual_seed(0)
     m, out = 24576, {}
     for name, n, k in (("up", 13824, 5120), ("down", 5120, 13824)):
@@ -104,12 +105,12 @@ def bench_c3(torch, ops, dev) -> dict:
         y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
 
         def quant(_i):
-            ops.quant_rows(x, ops.FMT_E4M3FN, codes=q_a, scales=s_a)
+            ops.quant_rows_tiled(x, ops.FMT_E4M3FN, codes=q_a, scales=s_a)
             ops.lora_down(x, la, out=t)
 
         def gemm(_i):
             ops.scaled_mm(q_a, qw, s_a.reshape(-1), sw.reshape(-1), lora_t=t, lora_b=lb, lora_scale=1.0, out=y,
-                          b_tiled=True)
+                          a_tiled=True, b_tiled=True, m=m)
 
         for f in (quant, gemm):
             f(0)

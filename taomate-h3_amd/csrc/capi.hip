@@ -360,7 +360,9 @@ __attribute__((visibility("default"))) int h3q_scaled_mm(int format, const void*
             return fail(H3Q_ERR_INVALID, "%s: unknown operand layout %d", who, layout);
     const bool a_tiled = a_layout == H3Q_LAYOUT_TILED, b_tiled = b_layout == H3Q_LAYOUT_TILED;
     if (int rc = check_gemm_operands(who, a, lda, b, ldb, m, n, k, 1, a_tiled, b_tiled)) return rc;
-    if (a_tiled && lora_t) return fail(H3Q_ERR_UNSUPPORTED, "%s: tiled activations take no LoRA epilogue", who);
+    if (a_tiled && lora_t && m <= h3q::kSkinnyMaxM)
+        return fail(H3Q_ERR_UNSUPPORTED, "%s: tiled activations with m <= %lld take no LoRA epilogue", who,
+                    (long long)h3q::kSkinnyMaxM);
     for (int kind : {a_scale_kind, b_scale_kind})
         if (kind != H3Q_SCALE_PER_ROW && kind != H3Q_SCALE_PER_TENSOR)
             return fail(H3Q_ERR_INVALID, "%s: unknown scale kind %d", who, kind);

@@ -71,10 +71,16 @@ constexpr int kW4ABytes = 256 * 64;              // A part of a stage
 // One wave copy (buffer_load_dwordx4 ... lds) with a scalar offset: lane L's
 // 16 bytes at src + voff + soff land at LDS byte lds_base + 16 L.  Inline
 // asm for the reason given at copy16 (h3q_common.hpp).
+// The scalar operands go through readfirstlane: they are uniform, and where
+// the compiler holds one in a VGPR (it may, in the LoRA instances) this moves
+// it to an SGPR; on a value already in SGPRs it folds away.
 __device__ __forceinline__ void copy16_soff(const CopySrc& src, uint32_t lds_base, uint32_t voff, uint32_t soff) {
+    const v4i d = {__builtin_amdgcn_readfirstlane(src.d[0]), __builtin_amdgcn_readfirstlane(src.d[1]),
+                   __builtin_amdgcn_readfirstlane(src.d[2]), __builtin_amdgcn_readfirstlane(src.d[3])};
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :
-                 : "s"(lds_base), "v"(voff), "s"(src.d), "s"(soff)
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(d),
+                   "s"(__builtin_amdgcn_readfirstlane(soff))
                  : "memory");
 }
 
@@ -135,7 +141,18 @@ struct W4Op<kOpInt8> {
 // idle for a full one.  A half tile runs the same ring and k order with two
 // 32-row blocks per wave (waves 2 x 2 of 64 x 128), so its outputs carry the
 // same bits as in a whole tile.
-template <int OP, bool BIAS, bool TA, bool TB, bool F16>
+//
+// LORA: out gains lora_scale * (t[m, :] . lora_b[n, :]) (bf16 t [M, r] and
+// lora_b [N, r], r <= 128) before the single rounding.  Each tile's copy
+// stream then carries four more groups after its k-steps: rank bytes
+// 64 l .. 64 l + 63 of t (as A) and of lora_b (as B), row-major, zero past
+// 2 r bytes.  After the last k-step the four groups fill the ring; every
+// 32 x 32 block takes 8 v_mfma_f32_32x32x16_bf16 over the rank in order
+// into a fresh accumulator L and stores fma(lora_scale, L,
+// s_a * (s_w * acc) [+ bias]) (the arithmetic of gemm_kernel's LoRA
+// epilogue); then the ring is primed again for the next tile (the rank
+// groups leave no stage free to prefetch into).
+template <int OP, bool BIAS, bool TA, bool TB, bool F16, bool LORA>
 __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m, int tiles_n, int split_tail) {
     using acc_t = typename W4Op<OP>::acc_t;
     using frag_t = typename W4Op<OP>::frag_t;
@@ -152,6 +169,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     const int wn0 = (wave & 1) * 128;
     const int g = lane >> 5, c32 = lane & 31;
     const int ksteps = (int)(p.k / 64);          // even: k % 128 == 0
+    const int ngroups = ksteps + (LORA ? 4 : 0); // copy groups per tile
     const int64_t steps128 = p.k / 128;          // tiled operands: 128-byte k-steps per block row
 
     // Work items j < nfull are whole tiles; item nfull (has_half) is a half tile.
@@ -229,6 +247,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
                      live ? a_bytes : 0u);
         rb = CopySrc((const uint8_t*)p.b + (TB ? (int64_t)(t.n0 / 16) * steps128 * 2048 : (int64_t)t.n0 * p.ldb),
                      live ? b_bytes : 0u);
+
         const int ln = opaque_lane();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -250,9 +269,38 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
             copy16(CopySrc(p.bias + t.n0, (uint32_t)t.cols * 2u), (uint32_t)(uintptr_t)(e + 2048),
                    lane < 32 ? 16u * lane : 0x80000000u);
     };
+    // LORA group l of the tile: 16 rows x 64 bytes per copy, row-major with a
+    // per-lane offset that includes the rank bytes (zero past 2 r).
+    auto lora_offset = [&](int c, int l, int rows, int64_t ld) __attribute__((always_inline)) -> uint32_t {
+        const int ln = opaque_lane();
+        const int row = c * 16 + (ln >> 2), chunk = (ln & 3) ^ swz64(ln >> 2);
+        const int kb = 64 * l + 16 * chunk;
+        return row < rows && kb < 2 * p.lora_rank ? (uint32_t)row * (uint32_t)(ld * 2) + (uint32_t)kb : 0x80000000u;
+    };
     // Copy q (0..3: A, 4..7: B) of the group for (cj, cs) into stage st.
-    auto issue_copy = [&](int q, int st) __attribute__((always_inline)) {
+    // rank: the group is a LORA rank group (the tile's last four steps issue
+    // those; a compile-time flag keeps the branch out of the other steps).
+    auto issue_copy = [&](int q, int st, auto rank) __attribute__((always_inline)) {
         const uint32_t base = ring_addr + (uint32_t)(st * kW4StageBytes);
+        if constexpr (decltype(rank)::value) {
+            // Descriptors of the copy tile's t / lora_b rows, built here so
+            // they hold no registers through the other steps.
+            const int l = cs - ksteps;
+            const bool live = cj < ntiles;
+            const TileSrc t = tile_src(live ? cj : ntiles - 1);
+            if (q < 4) {
+                const CopySrc lt((const uint8_t*)p.lora_t + (int64_t)t.m0 * p.ldt * 2,
+                                 live ? (uint32_t)(t.rows * p.ldt * 2) : 0u);
+                copy16_soff(lt, base + (uint32_t)((wave + 4 * q) * 1024), lora_offset(wave + 4 * q, l, t.rows, p.ldt),
+                            0u);
+            } else {
+                const CopySrc lb((const uint8_t*)p.lora_b + (int64_t)t.n0 * p.ldlb * 2,
+                                 live ? (uint32_t)(t.cols * p.ldlb * 2) : 0u);
+                copy16_soff(lb, base + (uint32_t)(kW4ABytes + (wave + 4 * (q - 4)) * 1024),
+                            lora_offset(wave + 4 * (q - 4), l, t.cols, p.ldlb), 0u);
+            }
+            return;
+        }
         const uint32_t soff_t = (uint32_t)((cs >> 1) * 2048 + (cs & 1) * 512), soff_r = (uint32_t)(cs * 64);
         if (q < 4)
             copy16_soff(ra, base + (uint32_t)((wave + 4 * q) * 1024), voff_a[q], TA ? soff_t : soff_r);
@@ -261,7 +309,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
                         TB ? soff_t : soff_r);
     };
     auto advance_copy = [&]() __attribute__((always_inline)) {
-        if (++cs == ksteps) {
+        if (++cs == ngroups) {
             cs = 0;
             ++cj;
             setup_copy_tile(cj);
@@ -339,7 +387,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     // in place by a scheduling barrier.  The reads of the next stage use the
     // layout of MI = 4 (a superset of a half tile's: the extra A blocks are
     // read and never used), so a step may prepare a half tile's first step.
-    auto body = [&](auto mi, bool first, const Frags& Fc, Frags& Fn, int rst, int cst) __attribute__((always_inline)) {
+    auto body = [&](auto mi, auto rank, bool first, const Frags& Fc, Frags& Fn, int rst, int cst)
+                    __attribute__((always_inline)) {
         constexpr int MI = decltype(mi)::value;
         constexpr int NM = 4 * MI * KS;                  // MFMAs per step per wave
         constexpr int NR = (4 + 4) * KS;                 // fragment reads per step
@@ -348,7 +397,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         for (int t = 0; t < NT; ++t) {
             if (t < NM) mfma(mi, first, Fc, t);
             if (t < NR) read_frag(std::integral_constant<int, 4>(), Fn, t, rst);
-            else if (t - NR < 8) issue_copy(t - NR, cst);
+            else if (t - NR < 8) issue_copy(t - NR, cst, rank);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -415,27 +464,102 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         }
     };
 
+    // ------------------------------------------------------------- LoRA
+    // epilogue of tile mj (LORA): group l of the rank sits in stage
+    // (ksteps + l) % 4; rank k-step s of a 64-byte stage row is logical chunk
+    // 2 s + g, as for the int8 fragments.  Each lane stores its four
+    // consecutive columns of a row as 8 bytes (the ring holds the rank groups,
+    // so there is no stage to stage the stores through).
+    auto lora_fold = [&](auto mi, int mj) __attribute__((always_inline)) {
+        constexpr int MI = decltype(mi)::value;
+        const int wm0 = (wave >> 1) * 32 * MI;
+        const int ln = opaque_lane();
+        const int gg = ln >> 5, cc = ln & 31;
+        const H3Q_LDS uint8_t* e = ep + (mj & 1) * 3072;
+        const TileSrc cur = tile_src(mj);
+        const __amdgpu_buffer_rsrc_t ro =
+            make_rsrc((uint8_t*)p.out + (int64_t)cur.m0 * p.ldo * 2, (uint32_t)((int64_t)cur.rows * p.ldo * 2));
+        uint32_t lra[2], lrb[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t chunk = (uint32_t)(((2 * h + gg) ^ swz64(cc)) << 4);
+            lra[h] = (uint32_t)((wm0 + cc) * 64) + chunk;
+            lrb[h] = (uint32_t)(kW4ABytes + (wn0 + cc) * 64) + chunk;
+        }
+        auto frag = [&](int l, int h, const uint32_t* off, int blk) __attribute__((always_inline)) -> v8bf {
+            const H3Q_LDS uint8_t* sb = ring + ((ksteps + l) & 3) * kW4StageBytes;
+            return __builtin_bit_cast(v8bf, ld16(sb + off[h] + blk * 2048));
+        };
+        // VALU reads of MFMA results: wait out the last MFMAs' passes.
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            v8bf tf[8];
+#pragma unroll
+            for (int x = 0; x < 8; ++x) tf[x] = frag(x >> 1, x & 1, lra, i);
+            const float sa = ((const H3Q_LDS float*)e)[wm0 + 32 * i + cc];
+            // The four column blocks' rank sums advance together (independent
+            // accumulators keep the MFMA pipe busy), each in rank order.
+            v16f L[4] = {};
+#pragma unroll
+            for (int x = 0; x < 8; ++x)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    L[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(x >> 1, x & 1, lrb, j), tf[x], L[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    // columns wn0 + 32 j + 8 q + 4 gg .. + 3 of row wm0 + 32 i + cc
+                    const int col = wn0 + 32 * j + 8 * q + 4 * gg;
+                    const v4f sw4 = *(const H3Q_LDS v4f*)(e + 1024 + 4 * col);
+                    v2u b4 = {0u, 0u};
+                    if constexpr (BIAS) b4 = *(const H3Q_LDS v2u*)(e + 2048 + 2 * col);
+                    float y[4];
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) {
+                        const float t = __fmul_rn(sw4[x], agpr_read(acc[i][j][4 * q + x]));
+                        float v;
+                        if constexpr (BIAS) v = __builtin_fmaf(sa, t, (x & 1) ? bf16_hi(b4[x >> 1]) : bf16_lo(b4[x >> 1]));
+                        else v = __fmul_rn(sa, t);
+                        y[x] = __builtin_fmaf(p.lora_scale, L[j][4 * q + x], v);
+                    }
+                    const uint32_t off = col < cur.cols
+                                             ? ((uint32_t)(wm0 + 32 * i + cc) * (uint32_t)p.ldo + (uint32_t)(cur.n0 + col)) * 2u
+                                             : 0xFFFFFFF0u;
+                    __builtin_amdgcn_raw_buffer_store_b64(v2u{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])}, ro, off,
+                                                          0, 0);
+                }
+            }
+        }
+    };
+
     // ------------------------------------------------------------ main loop
+    // Prime the ring: the copy cursor's next four groups into stages 0..3,
+    // then the fragments of stage 0.
+    auto prime = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int st = 0; st < kW4Stages; ++st) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) issue_copy(q, st, std::false_type());
+            advance_copy();
+        }
+        wait_vmcnt<(kW4Stages - 1) * 8>();
+        ring_barrier();
+#pragma unroll
+        for (int x = 0; x < 8 * KS; ++x) read_frag(std::integral_constant<int, 4>(), F0, x, 0);
+        wait_vmcnt<(kW4Stages - 2) * 8>();
+        ring_barrier();
+    };
     setup_copy_tile(0);
     issue_vectors(0);
-#pragma unroll
-    for (int st = 0; st < kW4Stages; ++st) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) issue_copy(q, st);
-        advance_copy();
-    }
     if (nfull == 0) to_half_layout();
-    wait_vmcnt<(kW4Stages - 1) * 8>();
-    ring_barrier();
-#pragma unroll
-    for (int x = 0; x < 8 * KS; ++x) read_frag(std::integral_constant<int, 4>(), F0, x, 0);
-    wait_vmcnt<(kW4Stages - 2) * 8>();
-    ring_barrier();
+    prime();
 
     int cur_st = 0;  // stage of the running step (its fragments are in registers)
-    auto step = [&](auto mi, bool first, const Frags& Fc, Frags& Fn) __attribute__((always_inline)) {
+    auto step = [&](auto mi, bool first, const Frags& Fc, Frags& Fn, auto rank) __attribute__((always_inline)) {
         const int nxt_st = cur_st + 1 == kW4Stages ? 0 : cur_st + 1;
-        body(mi, first, Fc, Fn, nxt_st, cur_st);
+        body(mi, rank, first, Fc, Fn, nxt_st, cur_st);
         advance_copy();
         wait_vmcnt<(kW4Stages - 2) * 8>();
         ring_barrier();
@@ -444,18 +568,50 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     // One tile: ksteps steps (the last one reads the next tile's first
     // fragments, in the half layout when a half tile follows), then the
     // epilogue through the stage that is free until the next step's copies.
+    // LORA: the last steps copy the rank groups instead; after the fold and
+    // the epilogue the ring is primed again from stage 0.
     auto run_tile = [&](auto mi, int mj, bool next_half) __attribute__((always_inline)) {
         const std::integral_constant<int, decltype(mi)::value> m;
-        step(m, true, F0, F1);
-        if (ksteps == 2 && next_half) to_half_layout();
-        step(m, false, F1, F0);
-        for (int s = 2; s < ksteps; s += 2) {
-            step(m, false, F0, F1);
-            if (s + 2 == ksteps && next_half) to_half_layout();
-            step(m, false, F1, F0);
+        const std::false_type op;
+        if constexpr (!LORA) {
+            step(m, true, F0, F1, op);
+            if (ksteps == 2 && next_half) to_half_layout();
+            step(m, false, F1, F0, op);
+            for (int s = 2; s < ksteps; s += 2) {
+                step(m, false, F0, F1, op);
+                if (s + 2 == ksteps && next_half) to_half_layout();
+                step(m, false, F1, F0, op);
+            }
+            epilogue(m, mj, cur_st);
+            ring_barrier();
+        } else {
+            // Step s copies group s + 4: the rank groups in steps ksteps - 4 ..
+            // ksteps - 1 (ksteps is even and at least 4).
+            const std::true_type rk;
+            if (ksteps > 4) {
+                step(m, true, F0, F1, op);
+                step(m, false, F1, F0, op);
+                for (int s = 2; s < ksteps - 4; s += 2) {
+                    step(m, false, F0, F1, op);
+                    step(m, false, F1, F0, op);
+                }
+                step(m, false, F0, F1, rk);
+            } else {
+                step(m, true, F0, F1, rk);
+            }
+            step(m, false, F1, F0, rk);
+            step(m, false, F0, F1, rk);
+            step(m, false, F1, F0, rk);
+            wait_vmcnt<0>();
+            ring_barrier();
+            lora_fold(m, mj);
+            ring_barrier();  // every wave is done with the rank groups
+            if (mj + 1 < ntiles) {
+                if (next_half) to_half_layout();
+                prime();
+                cur_st = 0;
+            }
         }
-        epilogue(m, mj, cur_st);
-        ring_barrier();
     };
     for (int mj = 0; mj < nfull; ++mj) run_tile(std::integral_constant<int, 4>(), mj, has_half && mj + 1 == nfull);
     if (has_half) run_tile(std::integral_constant<int, 2>(), nfull, false);
@@ -466,8 +622,10 @@ bool w4_supported(const GemmArgs& a) {
     // k in 128-byte steps (at least two, so each tile spans four ring stages),
     // 8-column bf16 stores, a 16-byte aligned output, and the 32-bit
     // block-relative offsets of the copies and stores.
-    if (a.lora_t || a.k % 128 || a.k < 256 || a.n % 8 || a.ldo % 8 || (uintptr_t)a.out % 16) return false;
+    if (a.k % 128 || a.k < 256 || a.n % 8 || a.ldo % 8 || (uintptr_t)a.out % 16) return false;
     if (a.out_f16 && a.a_tiled) return false;  // binary16 output: row-major activations only
+    // LoRA: bf16 output, rank <= 128 in steps of 8 (checked by the C ABI).
+    if (a.lora_t && (a.out_f16 || a.lora_rank > 128)) return false;
     if (a.m <= kSkinnyMaxM) return false;
     const int64_t tiled_block_row = (a.k / 128) * 2048 * 16;  // 256 rows of a tiled operand
     if ((a.a_tiled && tiled_block_row >= (int64_t(1) << 31)) || (a.b_tiled && tiled_block_row >= (int64_t(1) << 31)))
@@ -479,16 +637,27 @@ template <int OP, bool BIAS>
 static hipError_t launch_w4_op(const GemmArgs& a, hipStream_t st) {
     const int tiles_m = (int)((a.m + 255) / 256), tiles_n = (int)((a.n + 255) / 256);
     const dim3 grid((unsigned)persistent_grid(tiles_m * tiles_n));
-    if (a.out_f16) {
-        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, true, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
-        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, false, true>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
+#define H3Q_W4(TA, TB, F16, LORA) \
+    hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, TA, TB, F16, LORA>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1)
+    if (a.lora_t) {
+        if (a.a_tiled) {
+            if (a.b_tiled) H3Q_W4(true, true, false, true);
+            else H3Q_W4(true, false, false, true);
+        } else {
+            if (a.b_tiled) H3Q_W4(false, true, false, true);
+            else H3Q_W4(false, false, false, true);
+        }
+    } else if (a.out_f16) {
+        if (a.b_tiled) H3Q_W4(false, true, true, false);
+        else H3Q_W4(false, false, true, false);
     } else if (a.a_tiled) {
-        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, true, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
-        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, true, false, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
+        if (a.b_tiled) H3Q_W4(true, true, false, false);
+        else H3Q_W4(true, false, false, false);
     } else {
-        if (a.b_tiled) hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, true, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
-        else hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, false, false, false>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1);
+        if (a.b_tiled) H3Q_W4(false, true, false, false);
+        else H3Q_W4(false, false, false, false);
     }
+#undef H3Q_W4
     return hipGetLastError();
 }
 

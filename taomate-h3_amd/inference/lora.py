@@ -56,18 +56,20 @@ def fused_quantized_lora_linear(base: Any, inputs: torch.Tensor, lora_a: torch.T
             raise RuntimeError("H3 W8A8 supports bias-free linears only")
         workspace = getattr(base, "_cutlass_w8a8_workspace", None)
         if workspace is not None:
-            q, s, out = workspace.buffers(flat, int(base.weight.shape[0]))
+            _, s, out = workspace.buffers(flat, int(base.weight.shape[0]))
+            q = workspace._codes_buffer(flat)
         else:
             q = s = out = None
-        q, s = ops.quant_rows(flat, ops.FMT_INT8, ops.ROUND_RCP_MUL, codes=q, scales=s)
+        q, s, a_tiled = ops.quant_activations_for(flat, ops.FMT_INT8, ops.ROUND_RCP_MUL, base.weight, codes=q,
+                                                  scales=s, lora=True)
         w_scale = base._cutlass_w8a8_weight_scale
     else:
-        q, s = ops.quant_rows(flat, ops.FMT_E4M3FN, ops.ROUND_DIV)
+        q, s, a_tiled = ops.quant_activations_for(flat, ops.FMT_E4M3FN, ops.ROUND_DIV, base.weight, lora=True)
         out = None
         w_scale = base._fp8_w8a8_weight_scale
     out = ops.scaled_mm(q, base.weight, s.reshape(-1), w_scale.reshape(-1), bias=bias, lora_t=t,
-                        lora_b=lora_b.contiguous(), lora_scale=float(scale), out=out,
-                        b_tiled=ops.is_tiled(base.weight))
+                        lora_b=lora_b.contiguous(), lora_scale=float(scale), out=out, a_tiled=a_tiled,
+                        b_tiled=ops.is_tiled(base.weight), m=int(flat.shape[0]))
     return out.reshape(shape)
 
 

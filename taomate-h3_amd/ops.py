@@ -219,17 +219,19 @@ def check_layout(name: str, t: torch.Tensor, tiled: bool) -> None:
 
 
 def quant_activations_for(x: torch.Tensor, fmt: int, rounding: int, weight: torch.Tensor, *,
-                          codes: torch.Tensor | None = None, scales: torch.Tensor | None = None):
+                          codes: torch.Tensor | None = None, scales: torch.Tensor | None = None,
+                          lora: bool = False):
     """Per-token quantization of the 2-D activations of a linear whose weight
-    codes are ``weight`` (bf16 output, no LoRA): tiled when the weight is
-    tiled and the GEMM reads tiled activations at this shape -- the
-    weight-streaming GEMM for at most 128 tokens, the four-wave GEMM above
-    that (K >= 256, N a multiple of 8) -- else row-major.  Returns (codes,
-    scales, a_tiled); ``codes`` may be a larger workspace buffer of rows >=
-    tiled_rows(m)."""
+    codes are ``weight`` (bf16 output): tiled when the weight is tiled and the
+    GEMM reads tiled activations at this shape -- the weight-streaming GEMM
+    for at most 128 tokens (no LoRA), the four-wave GEMM above that (K >= 256,
+    N a multiple of 8, with or without the LoRA epilogue) -- else row-major.
+    Returns (codes, scales, a_tiled); ``codes`` may be a larger workspace
+    buffer of rows >= tiled_rows(m)."""
     m, k = x.shape
     n = int(weight.shape[0])
-    fits = 0 < m <= SKINNY_MAX_M or (m > SKINNY_MAX_M and k >= 256 and n % 8 == 0)
+    four_wave = m > SKINNY_MAX_M and k >= 256 and n % 8 == 0
+    fits = four_wave if lora else (0 < m <= SKINNY_MAX_M or four_wave)
     if is_tiled(weight) and k % 128 == 0 and fits:
         buf = None if codes is None else codes[:tiled_rows(m)]
         q, s = quant_rows_tiled(x, fmt, rounding, codes=buf, scales=scales)

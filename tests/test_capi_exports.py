@@ -65,11 +65,15 @@ def test_version_and_error_without_gpu():
     rc = lib.h3q_scaled_mm(0, None, 0, 1, None, 1, None, 0, 1, None, 1, None, None, 0, None, 0, 0, 1.0, None, 12,
                            256, 12, 256, None)
     assert rc == 2 and b"tiled activations" in lib.h3q_last_error()
-    # tiled activations take no LoRA epilogue
+    # tiled activations take the LoRA epilogue only above 128 rows (the
+    # four-wave GEMM); with 256 rows the call gets past that check
     p = ctypes.c_void_p(256)
     rc = lib.h3q_scaled_mm(0, None, 0, 1, None, 1, None, 0, 1, None, 1, None, p, 128, p, 128, 128, 1.0, None, 8,
-                           256, 8, 256, None)
+                           64, 8, 256, None)
     assert rc == 2 and b"LoRA" in lib.h3q_last_error()
+    rc = lib.h3q_scaled_mm(0, None, 0, 1, None, 1, None, 0, 1, None, 1, None, p, 128, p, 128, 128, 1.0, None, 8,
+                           256, 8, 256, None)
+    assert rc == 1 and b"null pointer" in lib.h3q_last_error()
     # 256 rows of a tiled operand must sit below a 32-bit offset: 256 * k < 2^31
     rc = lib.h3q_scaled_mm(0, None, 0, 1, None, 1, None, 0, 1, None, 1, None, None, 0, None, 0, 0, 1.0, None,
                            8, 4, 8, 1 << 23, None)

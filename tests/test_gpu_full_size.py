@@ -260,3 +260,40 @@ def test_split_tail_ragged_half_tiles(ops, oracle, device, fmt):
         rows = np.concatenate([np.arange(0, 256), np.arange(m - 1380, m)])
         rqa, rsa = oracle.quant_rows(bits16(x[torch.from_numpy(rows)]), "e4m3")
         _assert_fp8_close(oracle, bits16(out)[rows], rqa, rsa, rqw, rsw, bits16(bias))
+
+
+@pytest.mark.parametrize("fmt,rank,b_tiled,a_tiled", [("e4m3", 128, True, False), ("e4m3", 72, False, False),
+                                                    ("int8", 128, True, False), ("e4m3", 128, True, True),
+                                                    ("int8", 64, False, True)])
+def test_lora_epilogue_four_wave_equals_per_tile_kernel(ops, device, fmt, rank, b_tiled, a_tiled):
+    """The LoRA epilogue of the persistent four-wave GEMM against the per-tile
+    kernel's (reached through an output row stride that the four-wave GEMM
+    does not take): the same instructions in the same order, so every output
+    bit agrees.  m = 18 * 256 + 100, n = 4088: 304 tiles, a ragged last
+    tile-row and tile-column, the last round as half tiles; bias; rank 128
+    and ranks (72, 64) that leave rank groups partly or wholly empty; the
+    four-wave GEMM also with tiled activations (the per-tile kernel reads
+    them row-major)."""
+    m, n, k = 18 * 256 + 100, 4088, 512
+    f = ops.FMT_E4M3FN if fmt == "e4m3" else ops.FMT_INT8
+    ar = ops.ROUND_DIV if fmt == "e4m3" else ops.ROUND_RCP_MUL
+    print(f"LoRA four-wave vs per-tile {fmt} rank {rank} b_tiled={b_tiled} a_tiled={a_tiled}", flush=True)
+    x = activations(m, k, seed=31, outlier_channels=5, outlier_scale=15.0).to(device)
+    w = weights(n, k, seed=32).to(device)
+    gen = torch.Generator().manual_seed(33)
+    la = (torch.randn(rank, k, generator=gen) * 0.01).to(torch.bfloat16).to(device)
+    lb = (torch.randn(n, rank, generator=gen) * 0.01).to(torch.bfloat16).to(device)
+    bias = _bias(n, 34).to(device)
+    qa, sa = ops.quant_rows(x, f, ar)
+    qw, sw = ops.quant_rows_tiled(w, f, ops.ROUND_DIV) if b_tiled else ops.quant_rows(w, f, ops.ROUND_DIV)
+    t = ops.lora_down(x, la)
+    kw = dict(bias=bias, lora_t=t, lora_b=lb, lora_scale=0.75, b_tiled=b_tiled, n=n)
+    if a_tiled:
+        qat, _ = ops.quant_rows_tiled(x, f, ar)
+        four_wave = ops.scaled_mm(qat, qw, sa.reshape(-1), sw.reshape(-1), a_tiled=True, m=m, **kw)
+    else:
+        four_wave = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), **kw)
+    wide = torch.empty(m, n + 4, device=device, dtype=torch.bfloat16)
+    per_tile = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), out=wide[:, :n], **kw)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits16(four_wave), bits16(per_tile.contiguous()))
