@@ -70,9 +70,32 @@ constexpr uint32_t kOob = 0x80000000u;  // beyond every descriptor's range: load
 // ((wave * NB + j) * MT + t) * 64 + lane; wave w finishes the (j, t) tiles with
 // (j * MT + t) % WAVES == w: the sum over waves, then s_a * (s_w * acc) [+ bias]
 // to bf16, four consecutive columns per 8-byte store.
+// Epilogue vectors, copied into LDS by LDS-DMA when the kernel starts (so
+// the epilogue needs no memory round trip after the last MFMA): bytes
+// [0, 1024) the column scales of the workgroup's 16 * NB columns (or the
+// per-tensor scale), [1024, 1536) their bias, [1536, 2048) the row scales.
+// Buffer loads check their range per dword: a dword past the end reads 0.
+constexpr int kSkinnyVecBytes = 2048;
+template <int NB>
+__device__ __forceinline__ void skinny_vectors(const GemmArgs& p, H3Q_LDS uint8_t* vec, int64_t n0, int wave,
+                                               int lane, bool with_bias) {
+    const int64_t cols = (p.n - n0) < 16 * NB ? (p.n - n0) : 16 * NB;
+    const uint32_t base = (uint32_t)(uintptr_t)vec;
+    if (wave != 0) return;  // some configurations have only two waves
+    copy16(CopySrc(p.b_scale + (p.b_scale_per_col ? n0 : 0), (uint32_t)(p.b_scale_per_col ? cols : 1) * 4u), base,
+           16u * lane);
+    if (with_bias)
+        copy16(CopySrc(p.bias + n0, (uint32_t)cols * 2u), base + 1024u, lane < 32 ? 16u * lane : 0x80000000u);
+    copy16(CopySrc(p.a_scale, (uint32_t)(p.a_scale_per_row ? p.m : 1) * 4u), base + 1536u,
+           lane < 32 ? 16u * lane : 0x80000000u);
+}
+
 template <class acc_t, int MT, int NB, int WAVES, bool VEC, bool BIAS>
-__device__ __forceinline__ void skinny_epilogue(const GemmArgs& p, const H3Q_LDS acc_t* red, int64_t n0, int wave,
-                                                int lane) {
+__device__ __forceinline__ void skinny_epilogue(const GemmArgs& p, const H3Q_LDS uint8_t* vec,
+                                                const H3Q_LDS acc_t* red, int64_t n0, int wave, int lane) {
+    const H3Q_LDS float* vsw = (const H3Q_LDS float*)vec;
+    const H3Q_LDS uint16_t* vbias = (const H3Q_LDS uint16_t*)(vec + 1024);
+    const H3Q_LDS float* vsa = (const H3Q_LDS float*)(vec + 1536);
     const int r16 = lane & 15, kq = lane >> 4;
     const int64_t ldo = p.ldo;
     const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.out, (uint32_t)(p.m * ldo * 2));
@@ -83,8 +106,12 @@ __device__ __forceinline__ void skinny_epilogue(const GemmArgs& p, const H3Q_LDS
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const bool in = n + e < p.n;
-            sw[e] = in ? p.b_scale[p.b_scale_per_col ? n + e : 0] : 0.0f;
-            bias[e] = (BIAS || !VEC) && in && p.bias ? out_lo(p.bias[n + e], p.out_f16) : 0.0f;
+            const int nl = (int)(n + e - n0);
+            sw[e] = in ? vsw[p.b_scale_per_col ? nl : 0] : 0.0f;
+            // The LDS copy drops a dword that straddles the end of the bias
+            // (odd column counts, which only the scalar-store variant sees):
+            // that variant reads its bias from memory.
+            bias[e] = (BIAS || !VEC) && in && p.bias ? out_lo(VEC ? vbias[nl] : p.bias[n + e], p.out_f16) : 0.0f;
         }
         const bool has_bias = VEC ? BIAS : p.bias != nullptr;
 #pragma unroll
@@ -94,7 +121,7 @@ __device__ __forceinline__ void skinny_epilogue(const GemmArgs& p, const H3Q_LDS
 #pragma unroll
             for (int w = 1; w < WAVES; ++w) s += red[((w * NB + j) * MT + t) * 64 + lane];
             const int64_t m = 16 * t + r16;
-            const float sa = m < p.m ? p.a_scale[p.a_scale_per_row ? m : 0] : 0.0f;
+            const float sa = m < p.m ? vsa[p.a_scale_per_row ? m : 0] : 0.0f;
             float y[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -130,6 +157,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(GemmArgs p) {
     constexpr int RING = WAVES * D * SLOT;
     constexpr int RED = WAVES * NB * MT * 64 * (int)sizeof(acc_t);
     __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[RING > RED ? RING : RED];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_vec[kSkinnyVecBytes];
     H3Q_LDS uint8_t* const lds = (H3Q_LDS uint8_t*)lds_raw;
 
     const int lane = threadIdx.x & 63;
@@ -141,6 +169,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(GemmArgs p) {
     const CopySrc rw((const uint8_t*)p.b + n0 * p.ldb, (uint32_t)(rows_b * p.ldb));
     const CopySrc rx(p.a, (uint32_t)(p.m * p.lda));
 
+    skinny_vectors<NB>((const GemmArgs&)p, (H3Q_LDS uint8_t*)lds_vec, n0, wave, lane, (BIAS || !VEC) && p.bias);
     uint32_t woff[NB], xoff[MT];
 #pragma unroll
     for (int j = 0; j < NB; ++j) woff[j] = 16 * j + r16 < rows_b ? (uint32_t)((16 * j + r16) * p.ldb) : kOob;
@@ -210,7 +239,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(GemmArgs p) {
         for (int t = 0; t < MT; ++t) red[((wave * NB + j) * MT + t) * 64 + lane] = acc[j][t];
     __syncthreads();
 
-    skinny_epilogue<acc_t, MT, NB, WAVES, VEC, BIAS>(p, red, n0, wave, lane);
+    skinny_epilogue<acc_t, MT, NB, WAVES, VEC, BIAS>(p, (const H3Q_LDS uint8_t*)lds_vec, red, n0, wave, lane);
 }
 
 // Skinny GEMM over a tiled weight (and optionally tiled activations).  In the
@@ -227,6 +256,7 @@ template <int OP, int MT, int NB, int WAVES, int SPW, bool A_TILED, bool VEC, bo
 __global__ __launch_bounds__(WAVES * 64) void skinny_tiled_kernel(GemmArgs p) {
     using acc_t = typename SkinnyMfma<OP>::acc_t;
     __shared__ __attribute__((aligned(16))) acc_t red[WAVES * NB * MT * 64];
+    __shared__ __attribute__((aligned(16))) uint8_t lds_vec[kSkinnyVecBytes];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -241,6 +271,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_tiled_kernel(GemmArgs p) {
     const int64_t a_bytes = A_TILED ? (p.m + 15) / 16 * steps * 2048 : p.m * p.lda;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.a, (uint32_t)a_bytes);
 
+    skinny_vectors<NB>(p, (H3Q_LDS uint8_t*)lds_vec, n0, wave, lane, (BIAS || !VEC) && p.bias);
     uint32_t xoff[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
@@ -298,8 +329,10 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_tiled_kernel(GemmArgs p) {
     for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int t = 0; t < MT; ++t) red[((wave * NB + j) * MT + t) * 64 + lane] = acc[j][t];
+    wait_vmcnt0();  // the epilogue vectors' LDS copies (not tracked by the compiler)
     __syncthreads();
-    skinny_epilogue<acc_t, MT, NB, WAVES, VEC, BIAS>(p, (const H3Q_LDS acc_t*)red, n0, wave, lane);
+    skinny_epilogue<acc_t, MT, NB, WAVES, VEC, BIAS>(p, (const H3Q_LDS uint8_t*)lds_vec, (const H3Q_LDS acc_t*)red,
+                                                     n0, wave, lane);
 }
 
 namespace {
