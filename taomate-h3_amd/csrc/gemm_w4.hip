@@ -97,6 +97,29 @@ __device__ __forceinline__ void mfma_i8(v16i& c, const v4i& b, const v4i& a) {
 __device__ __forceinline__ void mfma_i8_first(v16i& c, const v4i& b, const v4i& a) {
     asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0" : "=a"(c) : "v"(b), "v"(a));
 }
+// bf16 rank step of the LoRA epilogue: c (binary32 values in the
+// accumulator registers, whatever acc_t says) += b x a.
+template <class acc_t>
+__device__ __forceinline__ void mfma_bf16(acc_t& c, const v4i& b, const v4i& a) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(b), "v"(a));
+}
+// An accumulator register read as the binary32 value it holds (LORA: after
+// the conversion every accumulator holds binary32, whatever acc_t says).
+__device__ __forceinline__ float agpr_bits(float x) {
+    float v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(x));
+    return v;
+}
+__device__ __forceinline__ float agpr_bits(int x) {
+    int v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(x));
+    return __int_as_float(v);
+}
+// Put 16 values computed in VGPRs into an accumulator's AGPRs.
+template <class acc_t>
+__device__ __forceinline__ void agpr_write(acc_t& c, const acc_t& v) {
+    asm volatile("; accumulator <- vgprs" : "=a"(c) : "0"(v));
+}
 __device__ __forceinline__ float agpr_read(float x) {
     float v;
     asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(x));
@@ -144,14 +167,15 @@ struct W4Op<kOpInt8> {
 //
 // LORA: out gains lora_scale * (t[m, :] . lora_b[n, :]) (bf16 t [M, r] and
 // lora_b [N, r], r <= 128) before the single rounding.  Each tile's copy
-// stream then carries four more groups after its k-steps: rank bytes
+// stream carries four more groups after its k-steps: rank bytes
 // 64 l .. 64 l + 63 of t (as A) and of lora_b (as B), row-major, zero past
-// 2 r bytes.  After the last k-step the four groups fill the ring; every
-// 32 x 32 block takes 8 v_mfma_f32_32x32x16_bf16 over the rank in order
-// into a fresh accumulator L and stores fma(lora_scale, L,
-// s_a * (s_w * acc) [+ bias]) (the arithmetic of gemm_kernel's LoRA
-// epilogue); then the ring is primed again for the next tile (the rank
-// groups leave no stage free to prefetch into).
+// 2 r bytes.  After the last k-step every accumulator becomes
+// y = s_a * (s_w * acc) [+ bias], divided by lora_scale unless that is 1
+// (times RN(1 / lora_scale)); then four rank steps run through the ring like
+// k-steps, each v_mfma_f32_32x32x16_bf16 adding t . lora_b to y in rank order,
+// and the epilogue stores bf16(lora_scale * acc) (acc itself when the scale is
+// 1).  The ring never drains: the rank steps' copy slots already carry the
+// next tile's first groups.
 template <int OP, bool BIAS, bool TA, bool TB, bool F16, bool LORA>
 __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m, int tiles_n, int split_tail) {
     using acc_t = typename W4Op<OP>::acc_t;
@@ -228,6 +252,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     // half tile's A rows past 128 are out of range too (zeros, never read).
     CopySrc ra(nullptr, 0), rb(nullptr, 0);
     uint32_t voff_a[4], voff_b[4];
+    // LORA: rows / columns of the copy tile, kept as scalars for the rank
+    // groups' descriptors (tile_src costs several integer divisions).
+    int cp_m0 = 0, cp_n0 = 0, cp_rows = 0, cp_cols = 0;
     int cj = 0, cs = 0;  // tile / k-step of the next copy group
     auto operand_offset = [&](bool tiled, int c, int sub_row, int pos, int ln, int rows, int64_t ld) __attribute__((always_inline)) -> uint32_t {
         if (tiled) {  // 16-row block c
@@ -248,6 +275,12 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         rb = CopySrc((const uint8_t*)p.b + (TB ? (int64_t)(t.n0 / 16) * steps128 * 2048 : (int64_t)t.n0 * p.ldb),
                      live ? b_bytes : 0u);
 
+        if constexpr (LORA) {
+            cp_m0 = t.m0;
+            cp_n0 = t.n0;
+            cp_rows = live ? t.rows : 0;  // no rows: the rank copies past the last tile read zeros
+            cp_cols = live ? t.cols : 0;
+        }
         const int ln = opaque_lane();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -283,21 +316,20 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     auto issue_copy = [&](int q, int st, auto rank) __attribute__((always_inline)) {
         const uint32_t base = ring_addr + (uint32_t)(st * kW4StageBytes);
         if constexpr (decltype(rank)::value) {
-            // Descriptors of the copy tile's t / lora_b rows, built here so
-            // they hold no registers through the other steps.
+            // Descriptors of the copy tile's t / lora_b rows, built here from
+            // the tile's scalars so they hold no registers through the other
+            // steps.
             const int l = cs - ksteps;
-            const bool live = cj < ntiles;
-            const TileSrc t = tile_src(live ? cj : ntiles - 1);
             if (q < 4) {
-                const CopySrc lt((const uint8_t*)p.lora_t + (int64_t)t.m0 * p.ldt * 2,
-                                 live ? (uint32_t)(t.rows * p.ldt * 2) : 0u);
-                copy16_soff(lt, base + (uint32_t)((wave + 4 * q) * 1024), lora_offset(wave + 4 * q, l, t.rows, p.ldt),
+                const CopySrc lt((const uint8_t*)p.lora_t + (int64_t)cp_m0 * p.ldt * 2,
+                                 (uint32_t)(cp_rows * p.ldt * 2));
+                copy16_soff(lt, base + (uint32_t)((wave + 4 * q) * 1024), lora_offset(wave + 4 * q, l, cp_rows, p.ldt),
                             0u);
             } else {
-                const CopySrc lb((const uint8_t*)p.lora_b + (int64_t)t.n0 * p.ldlb * 2,
-                                 live ? (uint32_t)(t.cols * p.ldlb * 2) : 0u);
+                const CopySrc lb((const uint8_t*)p.lora_b + (int64_t)cp_n0 * p.ldlb * 2,
+                                 (uint32_t)(cp_cols * p.ldlb * 2));
                 copy16_soff(lb, base + (uint32_t)(kW4ABytes + (wave + 4 * (q - 4)) * 1024),
-                            lora_offset(wave + 4 * (q - 4), l, t.cols, p.ldlb), 0u);
+                            lora_offset(wave + 4 * (q - 4), l, cp_cols, p.ldlb), 0u);
             }
             return;
         }
@@ -338,9 +370,21 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         rdb[h] = kW4ABytes + (TB ? (uint32_t)(((wn0 + c32) >> 4) * 1024 + tiled_off)
                                  : (uint32_t)((wn0 + c32) * 64 + ((chunk ^ swz64(c32)) << 4)));
     }
+    // Rank groups (LORA) sit row-major in the stage: rank k-step s of a
+    // 64-byte row is logical chunk 2 s + g, as for the int8 fragments.
+    uint32_t rra[2], rra_half[2], rrb[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t chunk = (uint32_t)(((2 * h + g) ^ swz64(c32)) << 4);
+        rra[h] = (uint32_t)(((wave >> 1) * 128 + c32) * 64) + chunk;
+        rra_half[h] = (uint32_t)(((wave >> 1) * 64 + c32) * 64) + chunk;
+        rrb[h] = (uint32_t)(kW4ABytes + (wn0 + c32) * 64) + chunk;
+    }
     auto to_half_layout = [&]() __attribute__((always_inline)) {
         rda[0] = rda_half[0];
         rda[1] = rda_half[1];
+        rra[0] = rra_half[0];
+        rra[1] = rra_half[1];
     };
     struct Frags {
         frag_t a[4 * KS], b[4 * KS];
@@ -368,6 +412,32 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         }
     };
 
+    // Rank fragment x (0..15) of stage st: x < 8 is t block x % 4, rank k-step
+    // x / 4; the rest lora_b block x % 4, k-step (x - 8) / 4.  Held in the
+    // fragment registers: e4m3 puts k-step s in lanes 4 s .. 4 s + 3 of the
+    // block's v8i, int8 in element y + 4 s.
+    auto read_rank = [&](Frags& F, int x, int st) __attribute__((always_inline)) {
+        const H3Q_LDS uint8_t* sb = ring + st * kW4StageBytes;
+        const bool is_a = x < 8;
+        const int y = x & 3, s = (x & 7) >> 2;
+        const v4i f = ld16(sb + (is_a ? rra[s] : rrb[s]) + y * 2048);
+        frag_t* dst = is_a ? F.a : F.b;
+        if constexpr (OP == kOpE4M3) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dst[y][4 * s + e] = f[e];
+        } else {
+            dst[y + 4 * s] = f;
+        }
+    };
+    auto rank_frag = [&](const frag_t* f, int y, int s) __attribute__((always_inline)) -> v4i {
+        if constexpr (OP == kOpE4M3) {
+            return s == 0 ? __builtin_shufflevector(f[y], f[y], 0, 1, 2, 3)
+                          : __builtin_shufflevector(f[y], f[y], 4, 5, 6, 7);
+        } else {
+            return f[y + 4 * s];
+        }
+    };
+
     acc_t acc[4][4];
     Frags F0, F1;
     // MFMA t of a step: acc[i][j] += b-fragment j x a-fragment i (k-step s).
@@ -387,17 +457,31 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     // in place by a scheduling barrier.  The reads of the next stage use the
     // layout of MI = 4 (a superset of a half tile's: the extra A blocks are
     // read and never used), so a step may prepare a half tile's first step.
-    auto body = [&](auto mi, auto rank, bool first, const Frags& Fc, Frags& Fn, int rst, int cst)
-                    __attribute__((always_inline)) {
+    // kind: 0 a k-step (MFMAs of the codes), 1 a LORA rank step (bf16 MFMAs);
+    // next: the fragments read for the next step are 0 codes, 1 rank.
+    auto body = [&](auto mi, auto rank, auto kind, auto next, bool first, const Frags& Fc, Frags& Fn, int rst,
+                    int cst) __attribute__((always_inline)) {
         constexpr int MI = decltype(mi)::value;
-        constexpr int NM = 4 * MI * KS;                  // MFMAs per step per wave
-        constexpr int NR = (4 + 4) * KS;                 // fragment reads per step
+        constexpr bool RANK = decltype(kind)::value != 0, NEXT_RANK = decltype(next)::value != 0;
+        constexpr int NM = RANK ? 8 * MI : 4 * MI * KS;          // MFMAs per step per wave
+        constexpr int NR = NEXT_RANK ? 16 : (4 + 4) * KS;        // fragment reads per step
         constexpr int NT = NM > NR + 8 ? NM : NR + 8;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            if (t < NM) mfma(mi, first, Fc, t);
-            if (t < NR) read_frag(std::integral_constant<int, 4>(), Fn, t, rst);
-            else if (t - NR < 8) issue_copy(t - NR, cst, rank);
+            if (t < NM) {
+                if constexpr (RANK) {
+                    const int s = t / (4 * MI), i = (t % (4 * MI)) / 4, j = t % 4;
+                    mfma_bf16(acc[i][j], rank_frag(Fc.b, j, s), rank_frag(Fc.a, i, s));
+                } else {
+                    mfma(mi, first, Fc, t);
+                }
+            }
+            if (t < NR) {
+                if constexpr (NEXT_RANK) read_rank(Fn, t, rst);
+                else read_frag(std::integral_constant<int, 4>(), Fn, t, rst);
+            } else if (t - NR < 8) {
+                issue_copy(t - NR, cst, rank);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -440,6 +524,11 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
                 float y[4];
 #pragma unroll
                 for (int x = 0; x < 4; ++x) {
+                    if constexpr (LORA) {  // y + t . lora_b, scaled back
+                        const float v = agpr_bits(acc[i][jj][4 * q + x]);
+                        y[x] = p.lora_scale == 1.0f ? v : __fmul_rn(p.lora_scale, v);
+                        continue;
+                    }
                     const float t = __fmul_rn(sw4[g16][x], agpr_read(acc[i][jj][4 * q + x]));
                     if constexpr (BIAS) {
                         const uint32_t w = b4[g16][x >> 1];
@@ -465,71 +554,44 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     };
 
     // ------------------------------------------------------------- LoRA
-    // epilogue of tile mj (LORA): group l of the rank sits in stage
-    // (ksteps + l) % 4; rank k-step s of a 64-byte stage row is logical chunk
-    // 2 s + g, as for the int8 fragments.  Each lane stores its four
-    // consecutive columns of a row as 8 bytes (the ring holds the rank groups,
-    // so there is no stage to stage the stores through).
-    auto lora_fold = [&](auto mi, int mj) __attribute__((always_inline)) {
+    // LORA, after the last k-step of tile mj: every accumulator becomes
+    // y = s_a * (s_w * acc) [+ bias] (the epilogue's arithmetic), times
+    // RN(1 / lora_scale) unless the scale is 1, as binary32 in the accumulator
+    // registers; the rank steps then add t . lora_b to it.
+    auto lora_convert = [&](auto mi, int mj) __attribute__((always_inline)) {
         constexpr int MI = decltype(mi)::value;
         const int wm0 = (wave >> 1) * 32 * MI;
         const int ln = opaque_lane();
         const int gg = ln >> 5, cc = ln & 31;
         const H3Q_LDS uint8_t* e = ep + (mj & 1) * 3072;
-        const TileSrc cur = tile_src(mj);
-        const __amdgpu_buffer_rsrc_t ro =
-            make_rsrc((uint8_t*)p.out + (int64_t)cur.m0 * p.ldo * 2, (uint32_t)((int64_t)cur.rows * p.ldo * 2));
-        uint32_t lra[2], lrb[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t chunk = (uint32_t)(((2 * h + gg) ^ swz64(cc)) << 4);
-            lra[h] = (uint32_t)((wm0 + cc) * 64) + chunk;
-            lrb[h] = (uint32_t)(kW4ABytes + (wn0 + cc) * 64) + chunk;
-        }
-        auto frag = [&](int l, int h, const uint32_t* off, int blk) __attribute__((always_inline)) -> v8bf {
-            const H3Q_LDS uint8_t* sb = ring + ((ksteps + l) & 3) * kW4StageBytes;
-            return __builtin_bit_cast(v8bf, ld16(sb + off[h] + blk * 2048));
-        };
+        const bool unit = p.lora_scale == 1.0f;
+        const float rs = unit ? 1.0f : 1.0f / p.lora_scale;
         // VALU reads of MFMA results: wait out the last MFMAs' passes.
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
-            v8bf tf[8];
-#pragma unroll
-            for (int x = 0; x < 8; ++x) tf[x] = frag(x >> 1, x & 1, lra, i);
             const float sa = ((const H3Q_LDS float*)e)[wm0 + 32 * i + cc];
-            // The four column blocks' rank sums advance together (independent
-            // accumulators keep the MFMA pipe busy), each in rank order.
-            v16f L[4] = {};
-#pragma unroll
-            for (int x = 0; x < 8; ++x)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    L[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag(x >> 1, x & 1, lrb, j), tf[x], L[j], 0, 0, 0);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
+                acc_t y;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    // columns wn0 + 32 j + 8 q + 4 gg .. + 3 of row wm0 + 32 i + cc
                     const int col = wn0 + 32 * j + 8 * q + 4 * gg;
                     const v4f sw4 = *(const H3Q_LDS v4f*)(e + 1024 + 4 * col);
                     v2u b4 = {0u, 0u};
                     if constexpr (BIAS) b4 = *(const H3Q_LDS v2u*)(e + 2048 + 2 * col);
-                    float y[4];
 #pragma unroll
                     for (int x = 0; x < 4; ++x) {
                         const float t = __fmul_rn(sw4[x], agpr_read(acc[i][j][4 * q + x]));
                         float v;
                         if constexpr (BIAS) v = __builtin_fmaf(sa, t, (x & 1) ? bf16_hi(b4[x >> 1]) : bf16_lo(b4[x >> 1]));
                         else v = __fmul_rn(sa, t);
-                        y[x] = __builtin_fmaf(p.lora_scale, L[j][4 * q + x], v);
+                        if (!unit) v = __fmul_rn(v, rs);
+                        if constexpr (OP == kOpE4M3) y[4 * q + x] = v;
+                        else y[4 * q + x] = __float_as_int(v);
                     }
-                    const uint32_t off = col < cur.cols
-                                             ? ((uint32_t)(wm0 + 32 * i + cc) * (uint32_t)p.ldo + (uint32_t)(cur.n0 + col)) * 2u
-                                             : 0xFFFFFFF0u;
-                    __builtin_amdgcn_raw_buffer_store_b64(v2u{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])}, ro, off,
-                                                          0, 0);
                 }
+                agpr_write(acc[i][j], y);
             }
         }
     };
@@ -557,9 +619,12 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     prime();
 
     int cur_st = 0;  // stage of the running step (its fragments are in registers)
-    auto step = [&](auto mi, bool first, const Frags& Fc, Frags& Fn, auto rank) __attribute__((always_inline)) {
+    const std::integral_constant<int, 0> codes_k;
+    const std::integral_constant<int, 1> rank_k;
+    auto step = [&](auto mi, bool first, const Frags& Fc, Frags& Fn, auto rank, auto kind, auto next)
+                    __attribute__((always_inline)) {
         const int nxt_st = cur_st + 1 == kW4Stages ? 0 : cur_st + 1;
-        body(mi, rank, first, Fc, Fn, nxt_st, cur_st);
+        body(mi, rank, kind, next, first, Fc, Fn, nxt_st, cur_st);
         advance_copy();
         wait_vmcnt<(kW4Stages - 2) * 8>();
         ring_barrier();
@@ -574,44 +639,43 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         const std::integral_constant<int, decltype(mi)::value> m;
         const std::false_type op;
         if constexpr (!LORA) {
-            step(m, true, F0, F1, op);
+            step(m, true, F0, F1, op, codes_k, codes_k);
             if (ksteps == 2 && next_half) to_half_layout();
-            step(m, false, F1, F0, op);
+            step(m, false, F1, F0, op, codes_k, codes_k);
             for (int s = 2; s < ksteps; s += 2) {
-                step(m, false, F0, F1, op);
+                step(m, false, F0, F1, op, codes_k, codes_k);
                 if (s + 2 == ksteps && next_half) to_half_layout();
-                step(m, false, F1, F0, op);
+                step(m, false, F1, F0, op, codes_k, codes_k);
             }
-            epilogue(m, mj, cur_st);
-            ring_barrier();
         } else {
             // Step s copies group s + 4: the rank groups in steps ksteps - 4 ..
-            // ksteps - 1 (ksteps is even and at least 4).
+            // ksteps - 1 (ksteps is even and at least 4), the next tile's first
+            // groups in the four rank steps.  The last k-step reads the first
+            // rank fragments; the last rank step the next tile's first ones.
             const std::true_type rk;
             if (ksteps > 4) {
-                step(m, true, F0, F1, op);
-                step(m, false, F1, F0, op);
+                step(m, true, F0, F1, op, codes_k, codes_k);
+                step(m, false, F1, F0, op, codes_k, codes_k);
                 for (int s = 2; s < ksteps - 4; s += 2) {
-                    step(m, false, F0, F1, op);
-                    step(m, false, F1, F0, op);
+                    step(m, false, F0, F1, op, codes_k, codes_k);
+                    step(m, false, F1, F0, op, codes_k, codes_k);
                 }
-                step(m, false, F0, F1, rk);
+                step(m, false, F0, F1, rk, codes_k, codes_k);
             } else {
-                step(m, true, F0, F1, rk);
+                step(m, true, F0, F1, rk, codes_k, codes_k);
             }
-            step(m, false, F1, F0, rk);
-            step(m, false, F0, F1, rk);
-            step(m, false, F1, F0, rk);
-            wait_vmcnt<0>();
-            ring_barrier();
-            lora_fold(m, mj);
-            ring_barrier();  // every wave is done with the rank groups
-            if (mj + 1 < ntiles) {
-                if (next_half) to_half_layout();
-                prime();
-                cur_st = 0;
-            }
+            step(m, false, F1, F0, rk, codes_k, codes_k);
+            step(m, false, F0, F1, rk, codes_k, codes_k);
+            step(m, false, F1, F0, rk, codes_k, rank_k);
+            lora_convert(m, mj);
+            step(m, false, F0, F1, op, rank_k, rank_k);
+            step(m, false, F1, F0, op, rank_k, rank_k);
+            step(m, false, F0, F1, op, rank_k, rank_k);
+            if (next_half) to_half_layout();
+            step(m, false, F1, F0, op, rank_k, codes_k);
         }
+        epilogue(m, mj, cur_st);
+        ring_barrier();
     };
     for (int mj = 0; mj < nfull; ++mj) run_tile(std::integral_constant<int, 4>(), mj, has_half && mj + 1 == nfull);
     if (has_half) run_tile(std::integral_constant<int, 2>(), nfull, false);
