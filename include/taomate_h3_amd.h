@@ -215,8 +215,9 @@ int h3q_quant_per_head_e4m3(const void* x, int64_t batch, int64_t seq, int64_t h
  * (one rounding of the fp32 result, torch._scaled_mm(out_dtype=float16),
  * FL/inference/fp8.py:135-143) instead of bf16 (not with LoRA).  a_layout / b_layout:
  * H3Q_LAYOUT_ROWS, or H3Q_LAYOUT_TILED (k % 128 == 0; the leading dimension
- * is then ignored; tiled activations without LoRA, and for m > 128 only with
- * k >= 256, n and ldo multiples of 8 and a 16-byte aligned out).  Tiled weights are the
+ * is then ignored; tiled activations for m <= 128 without LoRA, for m > 128
+ * with or without it, given k >= 256, n and ldo multiples of 8 and a 16-byte
+ * aligned bf16 out).  Tiled weights are the
  * fast format for every m (with few rows the GEMM streams them from HBM in
  * 1 KiB loads).  a_scale_kind / b_scale_kind: H3Q_SCALE_PER_ROW or
  * H3Q_SCALE_PER_TENSOR.  bias: bf16 [n] or NULL (added as one fused
