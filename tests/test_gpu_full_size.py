@@ -319,3 +319,75 @@ def test_lora_epilogue_four_wave_vs_per_tile_kernel(ops, device, fmt, rank, b_ti
     same = float(np.mean(bits16(four_wave) == bits16(per_tile.contiguous())))
     print(f"bit-identical to the per-tile kernel: {same:.5f}", flush=True)
     assert same >= 0.99, same
+
+
+@pytest.mark.parametrize("name,m,n,k", [("qkv_480p_phase3", 592, 10752, 5376),
+                                        ("fc1_1088p_phase3", 2640, 14336, 5376)])
+def test_h3_production_shapes_int8(ops, oracle, device, name, m, n, k):
+    """The production W8A8 path at real H3 shapes (TP-local QKV N = 10752 and
+    fc1 N = 14336, K = 5376 = 42 k-steps of 128; M per Ulysses rank from
+    H3/streaming/geometry.py:173-200, a multiple of 16 but not of 256):
+    per-token int8 activations (vLLM form) in the tiled layout, tiled int8
+    weights, no bias, as quant_activations_for feeds the four-wave GEMM.
+    Codes and bf16 outputs bit-exact on every 256-row tile-row's sampled rows,
+    the ragged last tile-row whole."""
+    print(f"H3 {name}: {m}x{n}x{k} int8", flush=True)
+    x = activations(m, k, seed=41, outlier_channels=k // 100, outlier_scale=15.0)
+    w = weights(n, k, seed=42)
+    xg = x.to(device)
+    qw, sw = _quant_weights(ops, w, device, "int8")
+    ops.mark_tiled(qw)  # as the module path records a packed weight
+    qa, sa, a_tiled = ops.quant_activations_for(xg, ops.FMT_INT8, ops.ROUND_RCP_MUL, qw)
+    assert a_tiled
+    out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), a_tiled=True, b_tiled=True, m=m, n=n)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([stratified_rows(m, seed=5), np.arange(m // 256 * 256, m)]))
+    rqa, rsa = oracle.quant_rows(bits16(x[torch.from_numpy(rows)]), "int8", "rcp")
+    rqw, rsw = oracle.quant_rows(bits16(w), "int8", "div")
+    np.testing.assert_array_equal(sw.cpu().numpy().ravel(), rsw)
+    np.testing.assert_array_equal(sa.cpu().numpy().ravel()[rows], rsa)
+    ref = oracle.epilogue(oracle.gemm_i8_i32(rqa, rqw), rsa, rsw)
+    np.testing.assert_array_equal(bits16(out)[rows], ref)
+
+
+def test_h3_production_shape_fp8_lora(ops, oracle, device):
+    """FL2VA's FP8 path with a rank-128 LoRA at a real shape: QKV at 768p
+    phase 0 (M = 3200, N = 10752, K = 5376), per-token x per-channel e4m3,
+    tiled activations and weights, the fused LoRA epilogue (scale 1.0), against
+    the reference's three rounding points (H3/inference/lora_checkpoint.py:196-205)
+    on the stratified rows plus the ragged last tile-row."""
+    m, n, k, rank = 3200, 10752, 5376, 128
+    print(f"H3 FP8 + LoRA {m}x{n}x{k}", flush=True)
+    x = activations(m, k, seed=43, outlier_channels=k // 100, outlier_scale=15.0)
+    w = weights(n, k, seed=44)
+    gen = torch.Generator().manual_seed(45)
+    la = (torch.randn(rank, k, generator=gen) * 0.01).to(torch.bfloat16)
+    lb = (torch.randn(n, rank, generator=gen) * 0.01).to(torch.bfloat16)
+    xg = x.to(device)
+    qw, sw = _quant_weights(ops, w, device, "e4m3")
+    ops.mark_tiled(qw)
+    qa, sa, a_tiled = ops.quant_activations_for(xg, ops.FMT_E4M3FN, ops.ROUND_DIV, qw, lora=True)
+    assert a_tiled
+    t = ops.lora_down(xg, la.to(device))
+    out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), lora_t=t, lora_b=lb.to(device), lora_scale=1.0,
+                        a_tiled=True, b_tiled=True, m=m, n=n)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([stratified_rows(m, seed=6), np.arange(m // 256 * 256, m)]))
+    xr = bits16(x[torch.from_numpy(rows)])
+    rqa, rsa = oracle.quant_rows(xr, "e4m3")
+    rqw, rsw = oracle.quant_rows(bits16(w), "e4m3")
+    model, rbound = oracle.gemm_e4m3_mfma(rqa, rqw)
+    base_f = oracle.bf16_to_f32(oracle.epilogue(model, rsa, rsw)).astype(np.float64)
+    t_gpu = oracle.bf16_to_f32(bits16(t)[rows]).astype(np.float64)
+    lbf = oracle.bf16_to_f32(bits16(lb)).astype(np.float64)
+    upd = oracle.bf16_to_f32(oracle.f32_to_bf16_fast((t_gpu @ lbf.T).astype(np.float32))).astype(np.float64)
+    ref = oracle.bf16_to_f32(oracle.f32_to_bf16_fast((base_f + upd).astype(np.float32))).astype(np.float64)
+    got = oracle.bf16_to_f32(bits16(out)[rows]).astype(np.float64)
+    scale = np.abs(rsa.astype(np.float64)).reshape(-1, 1) * np.abs(rsw.astype(np.float64)).reshape(1, -1)
+    upd_abs = np.abs(t_gpu) @ np.abs(lbf).T
+    bound = (bf16_ulp(base_f) + bf16_ulp(upd) + bf16_ulp(np.maximum(np.abs(ref), np.abs(got))) + rbound * scale
+             + 2.0 ** -22 * np.abs(base_f) + rank * 2.0 ** -24 * upd_abs + 2.0 ** -20 * (np.abs(base_f) + upd_abs))
+    err = np.abs(got - ref)
+    assert np.all(err <= bound), (err / bound).max()
+    assert np.mean(err <= bf16_ulp(np.abs(ref))) >= 0.99
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 2.0 ** -7
