@@ -457,23 +457,67 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     // in place by a scheduling barrier.  The reads of the next stage use the
     // layout of MI = 4 (a superset of a half tile's: the extra A blocks are
     // read and never used), so a step may prepare a half tile's first step.
-    // kind: 0 a k-step (MFMAs of the codes), 1 a LORA rank step (bf16 MFMAs);
+    // LORA, after the last k-step of a tile: accumulator block (i, j) becomes
+    // y = s_a * (s_w * acc) [+ bias] (the epilogue's arithmetic), times
+    // RN(1 / lora_scale) unless the scale is 1, as binary32 in the
+    // accumulator registers; the rank steps then add t . lora_b to it.  conv_e
+    // points at the tile's epilogue vectors.
+    const H3Q_LDS uint8_t* conv_e = ep;
+    auto convert_block = [&](auto mi, int i, int j) __attribute__((always_inline)) {
+        constexpr int MI = decltype(mi)::value;
+        const int wm0 = (wave >> 1) * 32 * MI;
+        const int gg = lane >> 5, cc = lane & 31;
+        const bool unit = p.lora_scale == 1.0f;
+        const float rs = unit ? 1.0f : 1.0f / p.lora_scale;
+        const float sa = ((const H3Q_LDS float*)conv_e)[wm0 + 32 * i + cc];
+        acc_t y;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int col = wn0 + 32 * j + 8 * q + 4 * gg;
+            const v4f sw4 = *(const H3Q_LDS v4f*)(conv_e + 1024 + 4 * col);
+            v2u b4 = {0u, 0u};
+            if constexpr (BIAS) b4 = *(const H3Q_LDS v2u*)(conv_e + 2048 + 2 * col);
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const float t = __fmul_rn(sw4[x], agpr_read(acc[i][j][4 * q + x]));
+                float v;
+                if constexpr (BIAS) v = __builtin_fmaf(sa, t, (x & 1) ? bf16_hi(b4[x >> 1]) : bf16_lo(b4[x >> 1]));
+                else v = __fmul_rn(sa, t);
+                if (!unit) v = __fmul_rn(v, rs);
+                if constexpr (OP == kOpE4M3) y[4 * q + x] = v;
+                else y[4 * q + x] = __float_as_int(v);
+            }
+        }
+        agpr_write(acc[i][j], y);
+    };
+    // kind: 0 a k-step (MFMAs of the codes), 1 a LORA rank step (bf16 MFMAs),
+    // 2 the first rank step, which converts block b in slot b and runs block
+    // b's first MFMA one slot later (the conversions' VALU work overlaps the
+    // MFMAs, and no MFMA reads an accumulator right after its VALU write);
     // next: the fragments read for the next step are 0 codes, 1 rank.
     auto body = [&](auto mi, auto rank, auto kind, auto next, bool first, const Frags& Fc, Frags& Fn, int rst,
                     int cst) __attribute__((always_inline)) {
         constexpr int MI = decltype(mi)::value;
-        constexpr bool RANK = decltype(kind)::value != 0, NEXT_RANK = decltype(next)::value != 0;
+        constexpr int KIND = decltype(kind)::value;
+        constexpr bool RANK = KIND != 0, CONV = KIND == 2, NEXT_RANK = decltype(next)::value != 0;
         constexpr int NM = RANK ? 8 * MI : 4 * MI * KS;          // MFMAs per step per wave
         constexpr int NR = NEXT_RANK ? 16 : (4 + 4) * KS;        // fragment reads per step
-        constexpr int NT = NM > NR + 8 ? NM : NR + 8;
+        constexpr int NMS = CONV ? NM + 1 : NM;                  // MFMA slots (the first one converts only)
+        constexpr int NT = NMS > NR + 8 ? NMS : NR + 8;
+        if constexpr (CONV) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            if (t < NM) {
+            if constexpr (CONV) {
+                if (t < 4 * MI) convert_block(mi, t / 4, t % 4);
+                __builtin_amdgcn_sched_barrier(0);  // the MFMA below reads the block converted one slot earlier
+            }
+            const int tm = CONV ? t - 1 : t;  // MFMA of this slot
+            if (tm >= 0 && tm < NM) {
                 if constexpr (RANK) {
-                    const int s = t / (4 * MI), i = (t % (4 * MI)) / 4, j = t % 4;
+                    const int s = tm / (4 * MI), i = (tm % (4 * MI)) / 4, j = tm % 4;
                     mfma_bf16(acc[i][j], rank_frag(Fc.b, j, s), rank_frag(Fc.a, i, s));
                 } else {
-                    mfma(mi, first, Fc, t);
+                    mfma(mi, first, Fc, tm);
                 }
             }
             if (t < NR) {
@@ -553,49 +597,6 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         }
     };
 
-    // ------------------------------------------------------------- LoRA
-    // LORA, after the last k-step of tile mj: every accumulator becomes
-    // y = s_a * (s_w * acc) [+ bias] (the epilogue's arithmetic), times
-    // RN(1 / lora_scale) unless the scale is 1, as binary32 in the accumulator
-    // registers; the rank steps then add t . lora_b to it.
-    auto lora_convert = [&](auto mi, int mj) __attribute__((always_inline)) {
-        constexpr int MI = decltype(mi)::value;
-        const int wm0 = (wave >> 1) * 32 * MI;
-        const int ln = opaque_lane();
-        const int gg = ln >> 5, cc = ln & 31;
-        const H3Q_LDS uint8_t* e = ep + (mj & 1) * 3072;
-        const bool unit = p.lora_scale == 1.0f;
-        const float rs = unit ? 1.0f : 1.0f / p.lora_scale;
-        // VALU reads of MFMA results: wait out the last MFMAs' passes.
-        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-#pragma unroll
-        for (int i = 0; i < MI; ++i) {
-            const float sa = ((const H3Q_LDS float*)e)[wm0 + 32 * i + cc];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc_t y;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int col = wn0 + 32 * j + 8 * q + 4 * gg;
-                    const v4f sw4 = *(const H3Q_LDS v4f*)(e + 1024 + 4 * col);
-                    v2u b4 = {0u, 0u};
-                    if constexpr (BIAS) b4 = *(const H3Q_LDS v2u*)(e + 2048 + 2 * col);
-#pragma unroll
-                    for (int x = 0; x < 4; ++x) {
-                        const float t = __fmul_rn(sw4[x], agpr_read(acc[i][j][4 * q + x]));
-                        float v;
-                        if constexpr (BIAS) v = __builtin_fmaf(sa, t, (x & 1) ? bf16_hi(b4[x >> 1]) : bf16_lo(b4[x >> 1]));
-                        else v = __fmul_rn(sa, t);
-                        if (!unit) v = __fmul_rn(v, rs);
-                        if constexpr (OP == kOpE4M3) y[4 * q + x] = v;
-                        else y[4 * q + x] = __float_as_int(v);
-                    }
-                }
-                agpr_write(acc[i][j], y);
-            }
-        }
-    };
-
     // ------------------------------------------------------------ main loop
     // Prime the ring: the copy cursor's next four groups into stages 0..3,
     // then the fragments of stage 0.
@@ -621,6 +622,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     int cur_st = 0;  // stage of the running step (its fragments are in registers)
     const std::integral_constant<int, 0> codes_k;
     const std::integral_constant<int, 1> rank_k;
+    const std::integral_constant<int, 2> conv_k;
     auto step = [&](auto mi, bool first, const Frags& Fc, Frags& Fn, auto rank, auto kind, auto next)
                     __attribute__((always_inline)) {
         const int nxt_st = cur_st + 1 == kW4Stages ? 0 : cur_st + 1;
@@ -667,8 +669,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
             step(m, false, F1, F0, rk, codes_k, codes_k);
             step(m, false, F0, F1, rk, codes_k, codes_k);
             step(m, false, F1, F0, rk, codes_k, rank_k);
-            lora_convert(m, mj);
-            step(m, false, F0, F1, op, rank_k, rank_k);
+            conv_e = ep + (mj & 1) * 3072;
+            step(m, false, F0, F1, op, conv_k, rank_k);
             step(m, false, F1, F0, op, rank_k, rank_k);
             step(m, false, F0, F1, op, rank_k, rank_k);
             if (next_half) to_half_layout();
