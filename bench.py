@@ -534,7 +534,7 @@ def main() -> int:
             "algorithmic_flops": flops,
         },
         "act_quant": {
-            "kernel": "h3q quant_rows_tiled_block_kernel (per-token e4m3fn, tiled codes)",
+            "kernel": "h3q quant_rows_tiled_img_kernel (per-token e4m3fn, tiled codes)",
             "bound": "hbm",
             "achieved": round(q_gbs, 1),
             "peak": HBM_PEAK_GBS,

@@ -77,25 +77,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(const uint16_t* __r
     }
 }
 
-// Tiled output by row blocks (K % 128 == 0, row0 % 16 == 0).  A workgroup of
-// ROWS waves (16: a whole 16-row block; 8: half of one) owns ROWS rows, one
-// per wave, each row held in VGPRs as in the kernel above.  In the tiled
-// layout a 16-row block's codes are one contiguous region (K / 128 tiles of
-// 2 KiB) and, inside each tile, the 8 rows of a half block fill 128-byte
-// segments.  So the codes are assembled in LDS 512 columns (four tiles) at a
-// time and written out with 16-byte stores, runs of ROWS consecutive threads
-// covering ROWS * 16 consecutive bytes, instead of the 8-byte pieces 256
-// bytes apart that a single row contributes to each tile.
-//
-// LDS image of a chunk: segment g of the 32 (tile, 1 KiB half, 16-row group
-// of the fragment) holds ROWS 16-byte slots, slot = segment * ROWS + row,
-// stored at slot s ^ ((s >> 4) & 15), which spreads a wave's slots (one row)
-// over the LDS banks and keeps the read-back conflict-free.  The image is
-// double-buffered with one barrier per chunk: a buffer's reads happen before
-// the next chunk's barrier, which every wave passes before it writes that
-// buffer again.  Each workgroup walks units u, u + grid, ...; with PREFETCH
-// the next unit's rows are loaded into a second register set while the
-// current one is packed and stored, so reads and writes overlap.
+// One row into NV 16-byte vectors per lane (zeros past the row's end).
 template <int NV>
 __device__ __forceinline__ void load_row(const uint16_t* __restrict__ x, int64_t ldx, int64_t row, int nvec,
                                          int lane, uint4 (&v)[NV]) {
@@ -104,77 +86,6 @@ __device__ __forceinline__ void load_row(const uint16_t* __restrict__ x, int64_t
     for (int i = 0; i < NV; ++i) {
         const int vec = i * 64 + lane;
         v[i] = vec < nvec ? xr[vec] : make_uint4(0, 0, 0, 0);
-    }
-}
-
-template <int FMT, int ROUND, int NV, int ROWS, bool PREFETCH>
-__global__ __launch_bounds__(ROWS * 64) void quant_rows_tiled_block_kernel(const uint16_t* __restrict__ x,
-                                                                           int64_t ldx, int64_t units, int k,
-                                                                           uint8_t* __restrict__ q, int64_t row0,
-                                                                           float* __restrict__ scales) {
-    static_assert(ROWS == 16 || ROWS == 8, "whole or half blocks");
-    constexpr int kChunkBytes = ROWS * 512;
-    __shared__ __attribute__((aligned(16))) uint8_t img[2][kChunkBytes];
-    const int lane = threadIdx.x & 63;
-    const int r = threadIdx.x >> 6;  // row within the unit
-    const int nvec = k >> 3;
-    const int64_t steps = k >> 7;
-    uint4 v[NV], vn[PREFETCH ? NV : 1];
-    int64_t u = blockIdx.x;
-    if (u < units) load_row<NV>(x, ldx, ROWS * u + r, nvec, lane, v);
-    while (u < units) {
-        const int64_t row = ROWS * u + r;
-        uint32_t m = 0;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            m = pk_abs_max(m, v[i].x);
-            m = pk_abs_max(m, v[i].y);
-            m = pk_abs_max(m, v[i].z);
-            m = pk_abs_max(m, v[i].w);
-        }
-        const float amax = wave_max(amax_from_packed(m));
-        RowQuant<FMT, ROUND> rq;
-        rq.init(amax);
-        if (lane == 0) scales[row] = rq.s;
-        const int64_t un = u + gridDim.x;
-        if constexpr (PREFETCH) {
-            if (un < units) load_row<NV>(x, ldx, ROWS * un + r, nvec, lane, vn);
-        }
-        const int64_t blk = (row0 >> 4) + (ROWS * u) / 16;
-        const int half = ROWS == 8 ? (int)(u & 1) : 0;
-        uint8_t* const qb = q + blk * steps * 2048;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            if (i * 512 >= k) break;
-            uint8_t* const buf = img[i & 1];
-            if (i * 64 + lane < nvec) {
-                const int kk = 8 * (lane & 15);  // byte within the 128-byte step
-                const int seg = (lane >> 4) * 8 + ((kk >> 4) & 1) * 4 + (kk >> 5);
-                const int slot = seg * ROWS + r;
-                const int phys = slot ^ ((slot >> 4) & 15);
-                uint2 out;
-                out.x = rq.pack4(v[i].x, v[i].y);
-                out.y = rq.pack4(v[i].z, v[i].w);
-                *reinterpret_cast<uint2*>(buf + phys * 16 + (kk & 8)) = out;
-            }
-            __syncthreads();
-            const int chunk = (k - i * 512) < 512 ? (k - i * 512) : 512;  // codes per row in this chunk
-            const int t = threadIdx.x;
-            if (t < chunk * ROWS / 16) {  // ROWS * chunk bytes in 16-byte slots
-                const int seg = t / ROWS, rr = t % ROWS;
-                const int off = (seg >> 3) * 2048 + ((seg >> 2) & 1) * 1024 + ((seg & 3) * 16 + 8 * half + rr) * 16;
-                const int phys = t ^ ((t >> 4) & 15);
-                *reinterpret_cast<uint4*>(qb + (int64_t)i * 8192 + off) = *reinterpret_cast<const uint4*>(buf + phys * 16);
-            }
-        }
-        __syncthreads();  // the image is reused by the next unit
-        if constexpr (PREFETCH) {
-#pragma unroll
-            for (int i = 0; i < NV; ++i) v[i] = vn[i];
-        } else if (un < units) {
-            load_row<NV>(x, ldx, ROWS * un + r, nvec, lane, v);
-        }
-        u = un;
     }
 }
 
@@ -302,23 +213,6 @@ static hipError_t launch_rows_vec(const uint16_t* x, int64_t ldx, int64_t rows, 
     return hipGetLastError();
 }
 
-template <int FMT, int ROUND, int NV, int ROWS, bool PREFETCH>
-static hipError_t launch_rows_tiled_units(const uint16_t* x, int64_t ldx, int64_t blocks, int64_t k, uint8_t* q,
-                                          int64_t row0, float* scales, int per_cu, hipStream_t st) {
-    const int64_t units = blocks * (16 / ROWS);
-    const int64_t cap = 256 * (int64_t)per_cu;
-    const int64_t grid = units < cap ? units : cap;
-    hipLaunchKernelGGL((quant_rows_tiled_block_kernel<FMT, ROUND, NV, ROWS, PREFETCH>), dim3((unsigned)grid),
-                       dim3(ROWS * 64), 0, st, x, ldx, units, (int)k, q, row0, scales);
-    return hipGetLastError();
-}
-
-// Half blocks (8 waves) throughout: measured on MI355X against whole blocks
-// (16 waves, one workgroup per CU), 25.6 vs 27.7 us at 8192 x 5120 and
-// 121.8 vs 127.0 us at 40960 x 5120 (row-major codes: 22.5 and 121.4 us).
-// Register budget of a lane: up to K = 6144 (NV <= 12) two rows fit in 128
-// VGPRs, so two workgroups share a CU; up to K = 14336 (NV <= 28) in 256,
-// one workgroup per CU; beyond that there is no prefetch.
 template <int FMT, int ROUND, int NV, bool PREFETCH>
 static hipError_t launch_rows_tiled_img_cfg(const uint16_t* x, int64_t ldx, int64_t blocks, int64_t k, uint8_t* q,
                                             int64_t row0, float* scales, int per_cu, hipStream_t st) {
@@ -346,16 +240,8 @@ static hipError_t launch_rows_tiled_img(const uint16_t* x, int64_t ldx, int64_t 
     return launch_rows_tiled_img_cfg<FMT, ROUND, NV, true>(x, ldx, blocks, k, q, row0, scales, per_cu, st);
 }
 
-template <int FMT, int ROUND, int NV>
-static hipError_t launch_rows_tiled_block(const uint16_t* x, int64_t ldx, int64_t blocks, int64_t k, uint8_t* q,
-                                          int64_t row0, float* scales, hipStream_t st) {
-    if constexpr (NV <= 12) return launch_rows_tiled_units<FMT, ROUND, NV, 8, true>(x, ldx, blocks, k, q, row0, scales, 2, st);
-    else if constexpr (NV <= 28) return launch_rows_tiled_units<FMT, ROUND, NV, 8, true>(x, ldx, blocks, k, q, row0, scales, 1, st);
-    else return launch_rows_tiled_units<FMT, ROUND, NV, 8, false>(x, ldx, blocks, k, q, row0, scales, 2, st);
-}
-
 template <int FMT, int ROUND>
-static hipError_t dispatch_rows_tiled_block(const uint16_t* x, int64_t ldx, int64_t blocks, int64_t k, uint8_t* q,
+static hipError_t dispatch_rows_tiled_img(const uint16_t* x, int64_t ldx, int64_t blocks, int64_t k, uint8_t* q,
                                             int64_t row0, float* scales, hipStream_t st) {
     const int64_t nv = (k + 511) / 512;
     if (nv <= 2) return launch_rows_tiled_img<FMT, ROUND, 2>(x, ldx, blocks, k, q, row0, scales, st);
@@ -376,12 +262,12 @@ static hipError_t dispatch_rows(const uint16_t* x, int64_t ldx, int64_t rows, in
     const bool aligned = (k % 8 == 0) && (ldx % 8 == 0) && (TILED || ldq % 8 == 0) &&
                          ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
     const int64_t nv = (k + 511) / 512;
-    // Tiled output from a block boundary: whole 16-row blocks by the block
+    // Tiled output from a block boundary: whole 16-row blocks by the image
     // kernel (16-byte aligned codes), the remaining rows below.
     if constexpr (TILED) {
         if (aligned && nv <= 32 && row0 % 16 == 0 && rows >= 16 && (uintptr_t)q % 16 == 0) {
             const int64_t blocks = rows / 16;
-            hipError_t e = dispatch_rows_tiled_block<FMT, ROUND>(x, ldx, blocks, k, q, row0, scales, st);
+            hipError_t e = dispatch_rows_tiled_img<FMT, ROUND>(x, ldx, blocks, k, q, row0, scales, st);
             if (e != hipSuccess || rows == 16 * blocks) return e;
             x += 16 * blocks * ldx;
             scales += 16 * blocks;

@@ -67,6 +67,14 @@ namespace {
 constexpr int kW4Stages = 4;
 constexpr int kW4StageBytes = (256 + 256) * 64;  // 32 KiB
 constexpr int kW4ABytes = 256 * 64;              // A part of a stage
+// Outputs of at least this many bytes are stored with the non-temporal cache
+// policy (gfx950 "nt"): they exceed what the caches could keep for a
+// consumer anyway, and without the hint their dirty lines stay in the
+// Infinity Cache and are written back under whatever runs next.  Measured at
+// c2 (252 MB of output, act-quant then GEMM): step 516-518 -> 499-500 us,
+// of which the following act-quant 37-38 -> 27-28 us and the GEMM 479 -> 472.
+constexpr int64_t kW4StreamOutBytes = int64_t(64) << 20;
+constexpr int kCachePolicyNT = 2;
 
 // One wave copy (buffer_load_dwordx4 ... lds) with a scalar offset: lane L's
 // 16 bytes at src + voff + soff land at LDS byte lds_base + 16 L.  Inline
@@ -153,7 +161,8 @@ struct W4Op<kOpInt8> {
 }  // namespace
 
 // F16: binary16 output and bias instead of bf16 (a separate instance, so the
-// bf16 epilogue carries no select).
+// bf16 epilogue carries no select).  stream_out: the output stores carry the
+// non-temporal cache policy.
 //
 // Schedule.  Workgroup b takes tiles b, b + G, ... (G = gridDim.x).  When the
 // last round of tiles is at most half full (0 < T % G <= G / 2 for T tiles)
@@ -177,7 +186,8 @@ struct W4Op<kOpInt8> {
 // 1).  The ring never drains: the rank steps' copy slots already carry the
 // next tile's first groups.
 template <int OP, bool BIAS, bool TA, bool TB, bool F16, bool LORA>
-__global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m, int tiles_n, int split_tail) {
+__global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m, int tiles_n, int split_tail,
+                                                        int stream_out) {
     using acc_t = typename W4Op<OP>::acc_t;
     using frag_t = typename W4Op<OP>::frag_t;
     constexpr int KS = W4Op<OP>::kSteps;
@@ -592,7 +602,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
                 const uint32_t off =
                     col_ok ? ((uint32_t)(wm0 + 32 * i + row) * (uint32_t)p.ldo + (uint32_t)(cur.n0 + col8)) * 2u
                            : 0xFFFFFFF0u;
-                __builtin_amdgcn_raw_buffer_store_b128(v, ro, off, 0, 0);
+                if (stream_out) __builtin_amdgcn_raw_buffer_store_b128(v, ro, off, 0, kCachePolicyNT);
+                else __builtin_amdgcn_raw_buffer_store_b128(v, ro, off, 0, 0);
             }
         }
     };
@@ -703,8 +714,10 @@ template <int OP, bool BIAS>
 static hipError_t launch_w4_op(const GemmArgs& a, hipStream_t st) {
     const int tiles_m = (int)((a.m + 255) / 256), tiles_n = (int)((a.n + 255) / 256);
     const dim3 grid((unsigned)persistent_grid(tiles_m * tiles_n));
+    const int stream_out = a.m * a.ldo * 2 >= kW4StreamOutBytes;
 #define H3Q_W4(TA, TB, F16, LORA) \
-    hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, TA, TB, F16, LORA>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1)
+    hipLaunchKernelGGL((gemm_w4_kernel<OP, BIAS, TA, TB, F16, LORA>), grid, dim3(256), 0, st, a, tiles_m, tiles_n, 1, \
+                       stream_out)
     if (a.lora_t) {
         if (a.a_tiled) {
             if (a.b_tiled) H3Q_W4(true, true, false, true);

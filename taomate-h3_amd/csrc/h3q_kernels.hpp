@@ -93,8 +93,9 @@ struct GemmArgs {
 hipError_t launch_gemm(int kind, bool raw_i32, const GemmArgs& args, hipStream_t st);
 
 // Persistent four-wave GEMM for large M (gemm_w4.hip): scaled e4m3 / int8 ->
-// bf16 with optional bias, no LoRA; row-major or tiled A and B; k % 128 == 0,
-// k >= 256, n % 8 == 0, ldo % 8 == 0, 16-byte aligned output, m > kSkinnyMaxM.
+// bf16 (or binary16) with optional bias and rank <= 128 LoRA; row-major or
+// tiled A and B; k % 128 == 0, k >= 256, n % 8 == 0, ldo % 8 == 0, 16-byte
+// aligned output, m > kSkinnyMaxM.
 // launch_gemm routes there itself when w4_supported() holds.
 bool w4_supported(const GemmArgs& a);
 hipError_t launch_gemm_w4(int kind, const GemmArgs& a, hipStream_t st);
