@@ -247,12 +247,14 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(GemmArgs p) {
 // contiguous in fragment order, so each half of a fragment is one fully
 // coalesced 1 KiB load straight into VGPRs.  A workgroup owns 16 * NB weight
 // rows; its waves split K (wave w takes steps w, w + WAVES, ...).  Each wave
-// issues the loads of SPW steps (W and A) before its first MFMA of that
-// chunk; sched_barrier keeps the compiler from sinking them next to their
-// uses, so a chunk is a single memory round trip per wave.  Row-major
+// works in chunks of SPW steps: it issues a chunk's loads (W and A) before
+// the chunk's first MFMA (sched_barrier keeps the compiler from sinking them
+// next to their uses), so a chunk costs one memory round trip; with PIPE two
+// register sets hold chunks c and c + 1, and chunk c + 1's loads are issued
+// before chunk c's MFMAs, so the round trips overlap.  Row-major
 // activations use the fragment mapping directly (row = lane % 16, 32 bytes at
 // 32 (lane / 16)).
-template <int OP, int MT, int NB, int WAVES, int SPW, bool A_TILED, bool VEC, bool BIAS>
+template <int OP, int MT, int NB, int WAVES, int SPW, bool PIPE, bool A_TILED, bool VEC, bool BIAS>
 __global__ __launch_bounds__(WAVES * 64) void skinny_tiled_kernel(GemmArgs p) {
     using acc_t = typename SkinnyMfma<OP>::acc_t;
     __shared__ __attribute__((aligned(16))) acc_t red[WAVES * NB * MT * 64];
@@ -286,18 +288,19 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_tiled_kernel(GemmArgs p) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[j][t] = acc_t{};
 
-    for (int c0 = 0; c0 < iters; c0 += SPW) {
-        v8i wf[SPW][NB], xf[SPW][MT];
+    // Chunk c: this wave's steps c * SPW .. c * SPW + SPW - 1 (step st at k
+    // bytes 128 st, st = chunk step * WAVES + wave); steps past K load zeros.
+    auto load_chunk = [&](int c, v8i (&wf)[SPW][NB], v8i (&xf)[SPW][MT]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int c = 0; c < SPW; ++c) {
-            const int64_t st = (int64_t)(c0 + c) * WAVES + wave;
+        for (int i = 0; i < SPW; ++i) {
+            const int64_t st = (int64_t)(c * SPW + i) * WAVES + wave;
             const bool in = st < steps;
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 const uint32_t o = in && j < nblk ? (uint32_t)((j * steps + st) * 2048 + 16 * lane) : kOob;
                 const v4u lo = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0));
                 const v4u hi = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rw, o == kOob ? kOob : o + 1024, 0, 0));
-                wf[c][j] = v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+                wf[i][j] = v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
             }
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
@@ -313,16 +316,45 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_tiled_kernel(GemmArgs p) {
                 }
                 const v4u lo = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, o0, 0, 0));
                 const v4u hi = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rx, o1, 0, 0));
-                xf[c][t] = v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+                xf[i][t] = v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
             }
         }
-        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto mfma_chunk = [&](const v8i (&wf)[SPW][NB], const v8i (&xf)[SPW][MT]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int c = 0; c < SPW; ++c)
+        for (int i = 0; i < SPW; ++i)
 #pragma unroll
             for (int j = 0; j < NB; ++j)
 #pragma unroll
-                for (int t = 0; t < MT; ++t) acc[j][t] = SkinnyMfma<OP>::run(wf[c][j], xf[c][t], acc[j][t]);
+                for (int t = 0; t < MT; ++t) acc[j][t] = SkinnyMfma<OP>::run(wf[i][j], xf[i][t], acc[j][t]);
+    };
+    const int nc = (iters + SPW - 1) / SPW;
+    if constexpr (PIPE) {
+        // Two register sets: the next chunk's loads are issued before the
+        // current chunk's MFMAs (sched_barrier keeps them there, and the
+        // compiler's vmcnt waits then leave the newer chunk in flight).  An
+        // even chunk count issues one chunk of out-of-range loads (zeros, no
+        // memory traffic) past the end.
+        v8i wa[SPW][NB], xa[SPW][MT], wb[SPW][NB], xb[SPW][MT];
+        load_chunk(0, wa, xa);
+        for (int c = 0; c + 1 < nc; c += 2) {
+            load_chunk(c + 1, wb, xb);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_chunk(wa, xa);
+            load_chunk(c + 2, wa, xa);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_chunk(wb, xb);
+        }
+        if (nc & 1) mfma_chunk(wa, xa);
+    } else {
+        // One register set: each chunk's loads, then its MFMAs (one round
+        // trip per chunk; with SPW * WAVES >= K / 128 there is one chunk).
+        for (int c = 0; c < nc; ++c) {
+            v8i wf[SPW][NB], xf[SPW][MT];
+            load_chunk(c, wf, xf);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_chunk(wf, xf);
+        }
     }
 
 #pragma unroll
@@ -352,17 +384,17 @@ hipError_t launch_skinny_cfg(const GemmArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
-template <int OP, int MT, int NB, int WAVES, int SPW, bool A_TILED>
+template <int OP, int MT, int NB, int WAVES, int SPW, bool PIPE, bool A_TILED>
 hipError_t launch_tiled_cfg(const GemmArgs& a, hipStream_t st) {
     const unsigned blocks = (unsigned)(((a.n + 15) / 16 + NB - 1) / NB);
     if (!a.out_vec)
-        hipLaunchKernelGGL((skinny_tiled_kernel<OP, MT, NB, WAVES, SPW, A_TILED, false, false>), dim3(blocks),
+        hipLaunchKernelGGL((skinny_tiled_kernel<OP, MT, NB, WAVES, SPW, PIPE, A_TILED, false, false>), dim3(blocks),
                            dim3(WAVES * 64), 0, st, a);
     else if (a.bias)
-        hipLaunchKernelGGL((skinny_tiled_kernel<OP, MT, NB, WAVES, SPW, A_TILED, true, true>), dim3(blocks),
+        hipLaunchKernelGGL((skinny_tiled_kernel<OP, MT, NB, WAVES, SPW, PIPE, A_TILED, true, true>), dim3(blocks),
                            dim3(WAVES * 64), 0, st, a);
     else
-        hipLaunchKernelGGL((skinny_tiled_kernel<OP, MT, NB, WAVES, SPW, A_TILED, true, false>), dim3(blocks),
+        hipLaunchKernelGGL((skinny_tiled_kernel<OP, MT, NB, WAVES, SPW, PIPE, A_TILED, true, false>), dim3(blocks),
                            dim3(WAVES * 64), 0, st, a);
     return hipGetLastError();
 }
@@ -371,13 +403,15 @@ hipError_t launch_tiled_cfg(const GemmArgs& a, hipStream_t st) {
 // activations, 12 rotating weight copies): 32 weight rows per workgroup beat
 // 16 once M >= 64 (each workgroup re-reads all of A from L2, so fewer
 // workgroups move fewer bytes): M = 64 11.6 us vs 15.0 us, M = 128 16.0 us vs
-// 20.5 us; M = 16 7.9 us.
+// 20.5 us; M = 16 7.9 us in one chunk per wave (8.2-9.9 us in two or more,
+// pipelined).  Pipelined single-step chunks: M = 64 11.3 us, M = 128 15.1 us
+// (against 11.6 and 15.8 without).
 template <int OP, bool A_TILED>
 hipError_t launch_tiled_op(const GemmArgs& a, hipStream_t st) {
-    if (a.m <= 16) return launch_tiled_cfg<OP, 1, 2, 4, 10, A_TILED>(a, st);
-    if (a.m <= 32) return launch_tiled_cfg<OP, 2, 2, 8, 5, A_TILED>(a, st);
-    if (a.m <= 64) return launch_tiled_cfg<OP, 4, 2, 8, 1, A_TILED>(a, st);
-    return launch_tiled_cfg<OP, 8, 2, 8, 1, A_TILED>(a, st);
+    if (a.m <= 16) return launch_tiled_cfg<OP, 1, 2, 4, 10, false, A_TILED>(a, st);
+    if (a.m <= 32) return launch_tiled_cfg<OP, 2, 2, 8, 5, false, A_TILED>(a, st);
+    if (a.m <= 64) return launch_tiled_cfg<OP, 4, 2, 8, 1, true, A_TILED>(a, st);
+    return launch_tiled_cfg<OP, 8, 2, 8, 1, true, A_TILED>(a, st);
 }
 
 // Row-major weights: the LDS-ring kernel above.
