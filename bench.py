@@ -88,11 +88,26 @@ def time_events(torch, fn, iters: int) -> float:
     return e0.elapsed_time(e1) / iters
 
 
+def time_in_step(torch, quant, gemm, iters: int):
+    """Average ms of quant() and of gemm() inside steps (quant, then gemm),
+    HIP events on the current stream around each, like the headline step."""
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(iters)]
+    for i in range(iters):
+        evs[i][0].record()
+        quant(i)
+        evs[i][1].record()
+        gemm(i)
+        evs[i][2].record()
+    torch.cuda.synchronize()
+    return (sum(e[0].elapsed_time(e[1]) for e in evs) / iters, sum(e[1].elapsed_time(e[2]) for e in evs) / iters)
+
+
 def bench_c3(torch, ops, dev) -> dict:
     """FFN at 768p, M=24576, up N=13824 K=5120 and down
     N=5120 K=13824, e4m3 per-token x per-channel (activation codes in the
     tiled layout), rank-128 LoRA (scale 1.0) added in the GEMM epilogue.
-    Times act-quant + LoRA down + scaled GEMM."""
+    Times act-quant + LoRA down + scaled GEMM inside steps (as the headline
+    step), and the GEMM back to back, where the MFMA clock settles lower."""
     gen = torch.Generator(device=dev).manual_seed(0)
     m, out = 24576, {}
     for name, n, k in (("up", 13824, 5120), ("down", 5120, 13824)):
@@ -112,14 +127,15 @@ def bench_c3(torch, ops, dev) -> dict:
             ops.scaled_mm(q_a, qw, s_a.reshape(-1), sw.reshape(-1), lora_t=t, lora_b=lb, lora_scale=1.0, out=y,
                           a_tiled=True, b_tiled=True, m=m)
 
-        for _ in range(6):  # steady clocks before timing (the headline step is warmed up likewise)
+        for _ in range(10):  # steady clocks before timing (the headline step is warmed up likewise)
             quant(0)
             gemm(0)
         torch.cuda.synchronize()
-        q_ms = time_events(torch, quant, 8)
-        g_ms = time_events(torch, gemm, 8)
+        q_ms, g_ms = time_in_step(torch, quant, gemm, 8)
+        b2b_ms = time_events(torch, gemm, 8)
         fl = 2.0 * m * n * k
         out[name] = {"M": m, "N": n, "K": k, "gemm_us": round(g_ms * 1e3, 1),
+                     "gemm_back_to_back_us": round(b2b_ms * 1e3, 1),
                      "gemm_fp8_tflops": round(fl / (g_ms * 1e-3) / 1e12, 1),
                      "pct_fp8_peak": round(100 * fl / (g_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 1),
                      "act_quant_plus_lora_down_us": round(q_ms * 1e3, 1),
@@ -316,7 +332,9 @@ def bench_f4(torch, ops, dev) -> dict:
 
 def bench_c5(torch, ops, dev) -> dict:
     """int8 W8A8 at 1080p, M=40960, K=N=5120: per-token
-    int8 act quant (vLLM formula) + int32-exact GEMM with fused dequant."""
+    int8 act quant (vLLM formula) + int32-exact GEMM with fused dequant.  The
+    GEMM is timed inside steps (act-quant, then GEMM) and back to back; the
+    act-quant back to back (its HBM figure)."""
     gen = torch.Generator(device=dev).manual_seed(0)
     m, n, k = 40960, 5120, 5120
     x = torch.randn(m, k, generator=gen, device=dev)
@@ -335,15 +353,16 @@ def bench_c5(torch, ops, dev) -> dict:
     def gemm(_i):
         ops.scaled_mm(q_a, qw, s_a.reshape(-1), sw.reshape(-1), out=y, a_tiled=True, b_tiled=True, m=m)
 
-    for _ in range(6):  # steady clocks before timing
+    for _ in range(10):  # steady clocks before timing
         quant(0)
         gemm(0)
     torch.cuda.synchronize()
+    _, g_ms = time_in_step(torch, quant, gemm, 8)
     q_ms = time_events(torch, quant, 8)
-    g_ms = time_events(torch, gemm, 8)
+    b2b_ms = time_events(torch, gemm, 8)
     ops_ = 2.0 * m * n * k
     q_bytes = 3 * m * k + 4 * m
-    return {"M": m, "N": n, "K": k, "gemm_us": round(g_ms * 1e3, 1),
+    return {"M": m, "N": n, "K": k, "gemm_us": round(g_ms * 1e3, 1), "gemm_back_to_back_us": round(b2b_ms * 1e3, 1),
             "gemm_int8_tops": round(ops_ / (g_ms * 1e-3) / 1e12, 1),
             "pct_int8_peak": round(100 * ops_ / (g_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 1),
             "act_quant_us": round(q_ms * 1e3, 1), "act_quant_GB/s": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
@@ -382,8 +401,10 @@ def cpu_baseline(torch, w_cpu, bias_cpu, x_cpu, budget_s: float = 12.0) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # Default warm-up of 40 steps (about 20 ms): after an idle spell the
+    # MFMA clock takes about 10 ms to settle at its loaded value.
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the c3 / c4 / c5 secondary measurements")
     ap.add_argument("--calibrate-copy", action="store_true",
