@@ -263,8 +263,10 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     CopySrc ra(nullptr, 0), rb(nullptr, 0);
     uint32_t voff_a[4], voff_b[4];
     // LORA: rows / columns of the copy tile, kept as scalars for the rank
-    // groups' descriptors (tile_src costs several integer divisions).
+    // groups' descriptors and offsets (tile_src costs several integer
+    // divisions).
     int cp_m0 = 0, cp_n0 = 0, cp_rows = 0, cp_cols = 0;
+    int rank_chunk16 = 0;  // LORA: byte of the lane's 16-byte chunk inside a rank group
     int cj = 0, cs = 0;  // tile / k-step of the next copy group
     auto operand_offset = [&](bool tiled, int c, int sub_row, int pos, int ln, int rows, int64_t ld) __attribute__((always_inline)) -> uint32_t {
         if (tiled) {  // 16-row block c
@@ -312,13 +314,21 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
             copy16(CopySrc(p.bias + t.n0, (uint32_t)t.cols * 2u), (uint32_t)(uintptr_t)(e + 2048),
                    lane < 32 ? 16u * lane : 0x80000000u);
     };
-    // LORA group l of the tile: 16 rows x 64 bytes per copy, row-major with a
-    // per-lane offset that includes the rank bytes (zero past 2 r).
-    auto lora_offset = [&](int c, int l, int rows, int64_t ld) __attribute__((always_inline)) -> uint32_t {
+    // LORA rank groups of the copy tile: once its k-step groups are all
+    // issued, ra / rb and voff_a / voff_b (free until the next tile's set-up)
+    // take the rows of t and lora_b, 16 rows x 64 bytes per copy, row-major;
+    // group l adds 64 l bytes as the scalar offset.
+    auto setup_rank_copies = [&]() __attribute__((always_inline)) {
+        ra = CopySrc((const uint8_t*)p.lora_t + (int64_t)cp_m0 * p.ldt * 2, (uint32_t)(cp_rows * p.ldt * 2));
+        rb = CopySrc((const uint8_t*)p.lora_b + (int64_t)cp_n0 * p.ldlb * 2, (uint32_t)(cp_cols * p.ldlb * 2));
         const int ln = opaque_lane();
-        const int row = c * 16 + (ln >> 2), chunk = (ln & 3) ^ swz64(ln >> 2);
-        const int kb = 64 * l + 16 * chunk;
-        return row < rows && kb < 2 * p.lora_rank ? (uint32_t)row * (uint32_t)(ld * 2) + (uint32_t)kb : 0x80000000u;
+        rank_chunk16 = 16 * ((ln & 3) ^ swz64(ln >> 2));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = (wave + 4 * i) * 16 + (ln >> 2);
+            voff_a[i] = row < cp_rows ? (uint32_t)row * (uint32_t)(p.ldt * 2) + (uint32_t)rank_chunk16 : 0x80000000u;
+            voff_b[i] = row < cp_cols ? (uint32_t)row * (uint32_t)(p.ldlb * 2) + (uint32_t)rank_chunk16 : 0x80000000u;
+        }
     };
     // Copy q (0..3: A, 4..7: B) of the group for (cj, cs) into stage st.
     // rank: the group is a LORA rank group (the tile's last four steps issue
@@ -326,21 +336,16 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     auto issue_copy = [&](int q, int st, auto rank) __attribute__((always_inline)) {
         const uint32_t base = ring_addr + (uint32_t)(st * kW4StageBytes);
         if constexpr (decltype(rank)::value) {
-            // Descriptors of the copy tile's t / lora_b rows, built here from
-            // the tile's scalars so they hold no registers through the other
-            // steps.
+            // Rank bytes 64 l + 16 chunk .. + 15 of the lane's row; zero past
+            // 2 r (a lane whose chunk starts there gets an out-of-range offset).
             const int l = cs - ksteps;
-            if (q < 4) {
-                const CopySrc lt((const uint8_t*)p.lora_t + (int64_t)cp_m0 * p.ldt * 2,
-                                 (uint32_t)(cp_rows * p.ldt * 2));
-                copy16_soff(lt, base + (uint32_t)((wave + 4 * q) * 1024), lora_offset(wave + 4 * q, l, cp_rows, p.ldt),
-                            0u);
-            } else {
-                const CopySrc lb((const uint8_t*)p.lora_b + (int64_t)cp_n0 * p.ldlb * 2,
-                                 (uint32_t)(cp_cols * p.ldlb * 2));
-                copy16_soff(lb, base + (uint32_t)(kW4ABytes + (wave + 4 * (q - 4)) * 1024),
-                            lora_offset(wave + 4 * (q - 4), l, cp_cols, p.ldlb), 0u);
-            }
+            const bool in = rank_chunk16 < 2 * (int)p.lora_rank - 64 * l;
+            if (q < 4)
+                copy16_soff(ra, base + (uint32_t)((wave + 4 * q) * 1024), in ? voff_a[q] : 0x80000000u,
+                            (uint32_t)(64 * l));
+            else
+                copy16_soff(rb, base + (uint32_t)(kW4ABytes + (wave + 4 * (q - 4)) * 1024),
+                            in ? voff_b[q - 4] : 0x80000000u, (uint32_t)(64 * l));
             return;
         }
         const uint32_t soff_t = (uint32_t)((cs >> 1) * 2048 + (cs & 1) * 512), soff_r = (uint32_t)(cs * 64);
@@ -473,20 +478,35 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     // accumulator registers; the rank steps then add t . lora_b to it.  conv_e
     // points at the tile's epilogue vectors.
     const H3Q_LDS uint8_t* conv_e = ep;
-    auto convert_block = [&](auto mi, int i, int j) __attribute__((always_inline)) {
+    // The blocks go column block by column block (j outer), so each lane
+    // reads the column scales and bias of a column block once (cw, cb) and
+    // its MI row scales once (ca).
+    float ca[4];
+    v4f cw[4];
+    v2u cb[4];
+    auto conv_row_scales = [&](auto mi) __attribute__((always_inline)) {
         constexpr int MI = decltype(mi)::value;
         const int wm0 = (wave >> 1) * 32 * MI;
-        const int gg = lane >> 5, cc = lane & 31;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) ca[i] = ((const H3Q_LDS float*)conv_e)[wm0 + 32 * i + (lane & 31)];
+    };
+    auto conv_col_vectors = [&](int j) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int col = wn0 + 32 * j + 8 * q + 4 * (lane >> 5);
+            cw[q] = *(const H3Q_LDS v4f*)(conv_e + 1024 + 4 * col);
+            if constexpr (BIAS) cb[q] = *(const H3Q_LDS v2u*)(conv_e + 2048 + 2 * col);
+        }
+    };
+    auto convert_block = [&](int i, int j) __attribute__((always_inline)) {
         const bool unit = p.lora_scale == 1.0f;
         const float rs = unit ? 1.0f : 1.0f / p.lora_scale;
-        const float sa = ((const H3Q_LDS float*)conv_e)[wm0 + 32 * i + cc];
+        const float sa = ca[i];
         acc_t y;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int col = wn0 + 32 * j + 8 * q + 4 * gg;
-            const v4f sw4 = *(const H3Q_LDS v4f*)(conv_e + 1024 + 4 * col);
-            v2u b4 = {0u, 0u};
-            if constexpr (BIAS) b4 = *(const H3Q_LDS v2u*)(conv_e + 2048 + 2 * col);
+            const v4f sw4 = cw[q];
+            const v2u b4 = cb[q];
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
                 const float t = __fmul_rn(sw4[x], agpr_read(acc[i][j][4 * q + x]));
@@ -501,9 +521,10 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         agpr_write(acc[i][j], y);
     };
     // kind: 0 a k-step (MFMAs of the codes), 1 a LORA rank step (bf16 MFMAs),
-    // 2 the first rank step, which converts block b in slot b and runs block
-    // b's first MFMA one slot later (the conversions' VALU work overlaps the
-    // MFMAs, and no MFMA reads an accumulator right after its VALU write);
+    // 2 the first rank step, which converts block b = (b % MI, b / MI) in slot
+    // b and runs block b's first MFMA one slot later (the conversions' VALU
+    // work overlaps the MFMAs, and no MFMA reads an accumulator right after
+    // its VALU write);
     // next: the fragments read for the next step are 0 codes, 1 rank.
     auto body = [&](auto mi, auto rank, auto kind, auto next, bool first, const Frags& Fc, Frags& Fn, int rst,
                     int cst) __attribute__((always_inline)) {
@@ -514,17 +535,26 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         constexpr int NR = NEXT_RANK ? 16 : (4 + 4) * KS;        // fragment reads per step
         constexpr int NMS = CONV ? NM + 1 : NM;                  // MFMA slots (the first one converts only)
         constexpr int NT = NMS > NR + 8 ? NMS : NR + 8;
-        if constexpr (CONV) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+        if constexpr (CONV) {
+            conv_row_scales(mi);
+            asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             if constexpr (CONV) {
-                if (t < 4 * MI) convert_block(mi, t / 4, t % 4);
+                if (t < 4 * MI) {
+                    if (t % MI == 0) conv_col_vectors(t / MI);
+                    convert_block(t % MI, t / MI);
+                }
                 __builtin_amdgcn_sched_barrier(0);  // the MFMA below reads the block converted one slot earlier
             }
             const int tm = CONV ? t - 1 : t;  // MFMA of this slot
             if (tm >= 0 && tm < NM) {
                 if constexpr (RANK) {
-                    const int s = tm / (4 * MI), i = (tm % (4 * MI)) / 4, j = tm % 4;
+                    const int s = tm / (4 * MI);
+                    // the converting step takes its first 4 MI MFMAs in conversion order
+                    const int i = CONV && s == 0 ? tm % MI : (tm % (4 * MI)) / 4;
+                    const int j = CONV && s == 0 ? tm / MI : tm % 4;
                     mfma_bf16(acc[i][j], rank_frag(Fc.b, j, s), rank_frag(Fc.a, i, s));
                 } else {
                     mfma(mi, first, Fc, tm);
@@ -665,6 +695,8 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
             // ksteps - 1 (ksteps is even and at least 4), the next tile's first
             // groups in the four rank steps.  The last k-step reads the first
             // rank fragments; the last rank step the next tile's first ones.
+            // The copy cursor runs four groups ahead: it reaches the rank
+            // groups (cs == ksteps) as step ksteps - 4 begins.
             const std::true_type rk;
             if (ksteps > 4) {
                 step(m, true, F0, F1, op, codes_k, codes_k);
@@ -673,8 +705,10 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
                     step(m, false, F0, F1, op, codes_k, codes_k);
                     step(m, false, F1, F0, op, codes_k, codes_k);
                 }
+                setup_rank_copies();
                 step(m, false, F0, F1, rk, codes_k, codes_k);
             } else {
+                setup_rank_copies();
                 step(m, true, F0, F1, rk, codes_k, codes_k);
             }
             step(m, false, F1, F0, rk, codes_k, codes_k);
