@@ -179,12 +179,12 @@ struct W4Op<kOpInt8> {
 // stream carries four more groups after its k-steps: rank bytes
 // 64 l .. 64 l + 63 of t (as A) and of lora_b (as B), row-major, zero past
 // 2 r bytes.  After the last k-step every accumulator becomes
-// y = s_a * (s_w * acc) [+ bias], divided by lora_scale unless that is 1
-// (times RN(1 / lora_scale)); then four rank steps run through the ring like
-// k-steps, each v_mfma_f32_32x32x16_bf16 adding t . lora_b to y in rank order,
-// and the epilogue stores bf16(lora_scale * acc) (acc itself when the scale is
-// 1).  The ring never drains: the rank steps' copy slots already carry the
-// next tile's first groups.
+// y = s_a * (s_w * acc) [+ bias] times RN(1 / lora_scale) (exactly y when
+// the scale is 1); then four rank steps run through the ring like k-steps,
+// each v_mfma_f32_32x32x16_bf16 adding t . lora_b to y in rank order, and the
+// epilogue stores bf16(lora_scale * acc) (acc itself when the scale is 1).
+// The ring never drains: the rank steps' copy slots already carry the next
+// tile's first groups.
 template <int OP, bool BIAS, bool TA, bool TB, bool F16, bool LORA>
 __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m, int tiles_n, int split_tail,
                                                         int stream_out) {
@@ -499,8 +499,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
         }
     };
     auto convert_block = [&](int i, int j) __attribute__((always_inline)) {
-        const bool unit = p.lora_scale == 1.0f;
-        const float rs = unit ? 1.0f : 1.0f / p.lora_scale;
+        // RN(1 / lora_scale) is 1 for a unit scale, and v * 1 = v exactly, so
+        // the multiply runs unconditionally (a select would cost as much).
+        const float rs = 1.0f / p.lora_scale;
         const float sa = ca[i];
         acc_t y;
 #pragma unroll
@@ -513,7 +514,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
                 float v;
                 if constexpr (BIAS) v = __builtin_fmaf(sa, t, (x & 1) ? bf16_hi(b4[x >> 1]) : bf16_lo(b4[x >> 1]));
                 else v = __fmul_rn(sa, t);
-                if (!unit) v = __fmul_rn(v, rs);
+                v = __fmul_rn(v, rs);
                 if constexpr (OP == kOpE4M3) y[4 * q + x] = v;
                 else y[4 * q + x] = __float_as_int(v);
             }
@@ -610,7 +611,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
                 for (int x = 0; x < 4; ++x) {
                     if constexpr (LORA) {  // y + t . lora_b, scaled back
                         const float v = agpr_bits(acc[i][jj][4 * q + x]);
-                        y[x] = p.lora_scale == 1.0f ? v : __fmul_rn(p.lora_scale, v);
+                        y[x] = __fmul_rn(p.lora_scale, v);  // exact for a unit scale
                         continue;
                     }
                     const float t = __fmul_rn(sw4[g16][x], agpr_read(acc[i][jj][4 * q + x]));
