@@ -474,9 +474,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
     // read and never used), so a step may prepare a half tile's first step.
     // LORA, after the last k-step of a tile: accumulator block (i, j) becomes
     // y = s_a * (s_w * acc) [+ bias] (the epilogue's arithmetic), times
-    // RN(1 / lora_scale) unless the scale is 1, as binary32 in the
-    // accumulator registers; the rank steps then add t . lora_b to it.  conv_e
-    // points at the tile's epilogue vectors.
+    // RN(1 / lora_scale), as binary32 in the accumulator registers; the rank
+    // steps then add t . lora_b to it.  conv_e points at the tile's epilogue
+    // vectors.
     const H3Q_LDS uint8_t* conv_e = ep;
     // The blocks go column block by column block (j outer), so each lane
     // reads the column scales and bias of a column block once (cw, cb) and
