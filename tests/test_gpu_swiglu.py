@@ -88,6 +88,25 @@ def test_special_values(ops, oracle, device):
     np.testing.assert_array_equal(bits16(out), oracle.swiglu(bits16(x)))
 
 
+def test_every_bf16_gate(ops, oracle, device):
+    """silu depends on the gate alone, so the 65536 bf16 gate values (NaNs,
+    infinities, subnormals and both zeros included) with up = 1 cover it
+    completely: y = bf16(silu(gate)) bit-exact against the oracle, whose exp
+    is the IEEE-only restatement while the kernel uses the hardware exp2.
+    NaN gates must give NaN (the payload is not compared)."""
+    gate = np.arange(65536, dtype=np.uint32).astype(np.uint16).reshape(64, 1024)
+    up = np.full((64, 1024), 0x3F80, dtype=np.uint16)  # bf16 1.0
+    xb = np.concatenate([gate, up], axis=1)
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)
+    print("swiglu every bf16 gate (64 x 1024, up = 1)", flush=True)
+    out, _, _ = ops.swiglu_quant(x.to(device), out=True)
+    torch.cuda.synchronize()
+    got, want = bits16(out), oracle.swiglu(xb)
+    nan_got, nan_want = (got & 0x7FFF) > 0x7F80, (want & 0x7FFF) > 0x7F80
+    np.testing.assert_array_equal(nan_got, nan_want)
+    np.testing.assert_array_equal(np.where(nan_want, 0, got), np.where(nan_want, 0, want))
+
+
 def test_torch_eager_on_the_gpu_within_tolerance(ops, device):
     """The reference's eager expression F.silu(gate) * up evaluated by torch on
     the same GPU (its own exp): every output within 1 bf16 ulp, >= 99.9% identical."""
