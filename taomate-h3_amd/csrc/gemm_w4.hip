@@ -571,7 +571,7 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(GemmArgs p, int tiles_m
                 if constexpr (NEXT_RANK) read_rank(Fn, t, rst);
                 else read_frag(std::integral_constant<int, 4>(), Fn, t, rst);
             }
-            if (t % CP == CP - 1) issue_copy(t / CP, cst, rank);
+            if (t % CP == CP - 1 && t / CP < 8) issue_copy(t / CP, cst, rank);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
