@@ -638,6 +638,12 @@ using TileBigLora = Tile<256, 256, 128, 2, 2, 4, 2>;
 // measured on MI355X at M = 24576, r = 128: K = 13824 164 us and K = 5120
 // 58 us, against 197 us and 67 us with 64-byte k-tiles.
 using TileLora = Tile<128, 128, 128, 4, 2, 2>;
+// Up to 256 x 96 rows the down-projection takes 96-row blocks (four waves of
+// 96 x 32, a 5-deep ring of 28 KiB stages), so that up to 256 workgroups
+// share the stream instead of M / 128 (M = 24576, same box, alternating:
+// K = 5120 60.4-61.5 us against 65.5-66.1; K = 13824 181-188 against
+// 185-186, no change).
+using TileLora96 = Tile<96, 128, 128, 5, 1, 4>;
 
 hipError_t launch_gemm(int kind, bool raw_i32, const GemmArgs& args, hipStream_t st) {
     GemmArgs a = args;
@@ -653,6 +659,9 @@ hipError_t launch_gemm(int kind, bool raw_i32, const GemmArgs& args, hipStream_t
                              : launch_tile<TileBig, kOpInt8, kEpiI32, false, false, false>(a, st);
         return lora ? launch_scaled<TileBigLora, kOpInt8, true>(a, st) : launch_scaled<TileBig, kOpInt8, false>(a, st);
     }
+    if ((a.m + 95) / 96 <= 256)
+        return a.out_vec ? launch_tile<TileLora96, kOpBF16, kEpiBF16, false, true, false>(a, st)
+                         : launch_tile<TileLora96, kOpBF16, kEpiBF16, false, false, false>(a, st);
     return a.out_vec ? launch_tile<TileLora, kOpBF16, kEpiBF16, false, true, false>(a, st)
                      : launch_tile<TileLora, kOpBF16, kEpiBF16, false, false, false>(a, st);
 }
