@@ -253,6 +253,21 @@ int h3q_lora_down(const void* x, int64_t ldx, const void* lora_a, int64_t lda, v
                   int64_t k, int64_t rank, void* stream);
 
 /*
+ * The same product split over K when x has few rows (below 128 blocks of 96):
+ * each K slice's binary32 partial goes to the caller's workspace, then the
+ * slices are summed in order and rounded once to bf16 (within the same error
+ * bound as h3q_lora_down; deterministic).  h3q_lora_down_workspace_bytes gives
+ * the bytes needed (0: the call does not split and needs no workspace); a
+ * smaller workspace is an error.  No counterpart in the reference: the
+ * reference's F.linear (H3/inference/lora_checkpoint.py:197-199) leaves this
+ * to the BLAS library; the split keeps the H3 shapes (M = 592 .. 6224 tokens)
+ * from running on a few dozen workgroups.
+ */
+int64_t h3q_lora_down_workspace_bytes(int64_t m, int64_t k, int64_t rank);
+int h3q_lora_down_ws(const void* x, int64_t ldx, const void* lora_a, int64_t lda, void* t, int64_t ldt, int64_t m,
+                     int64_t k, int64_t rank, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Fused RMSNorm + AdaLN modulate + per-token quantization: the producer of the
  * QKV input of a DiT block, fused_rms_norm_modulate
  * (H3/inference/fused_kernels.py:287-317 kernel, 700-730 wrapper), with the

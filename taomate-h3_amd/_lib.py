@@ -36,6 +36,8 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
                            _I64, _I64, _I64, _I64, _P]),
     "h3q_gemm_i8_i32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P]),
     "h3q_lora_down": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P]),
+    "h3q_lora_down_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    "h3q_lora_down_ws": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
     "h3q_rms_norm_modulate_quant": (_I, [_P, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _F, _P, _I64, _I, _I, _P, _I64,
                                          _P, _P]),
     "h3q_residual_gate_rms_norm_modulate_quant": (_I, [_P, _I64, _P, _I64, _P, _P, _P, _P, _I64, _P, _I64, _I64, _F,

@@ -443,10 +443,8 @@ __attribute__((visibility("default"))) int h3q_gemm_i8_i32(const void* a, int64_
     return check_launch(h3q::launch_gemm(h3q::kOpInt8, true, g, (hipStream_t)stream), who);
 }
 
-__attribute__((visibility("default"))) int h3q_lora_down(const void* x, int64_t ldx, const void* lora_a,
-                                                         int64_t lda, void* t, int64_t ldt, int64_t m, int64_t k,
-                                                         int64_t rank, void* stream) {
-    const char* who = "h3q_lora_down";
+static int lora_down_args(const char* who, const void* x, int64_t ldx, const void* lora_a, int64_t lda, void* t,
+                          int64_t ldt, int64_t m, int64_t k, int64_t rank, h3q::GemmArgs& g) {
     if (k % 8) return fail(H3Q_ERR_INVALID, "%s: k=%lld must be a multiple of 8", who, (long long)k);
     if (m < 0 || k < 0 || rank <= 0) return fail(H3Q_ERR_INVALID, "%s: bad shape", who);
     if (ldx < k || lda < k || ldt < rank) return fail(H3Q_ERR_INVALID, "%s: leading dimension too small", who);
@@ -455,9 +453,9 @@ __attribute__((visibility("default"))) int h3q_lora_down(const void* x, int64_t 
         return fail(H3Q_ERR_INVALID, "%s: x / lora_a rows must be 16-byte aligned", who);
     if (ldx * 2 >= (int64_t(1) << 23) || lda * 2 >= (int64_t(1) << 23))
         return fail(H3Q_ERR_UNSUPPORTED, "%s: row stride above 8 MiB", who);
-    if (m == 0) return ok();
+    if (m == 0) return H3Q_OK;
     if (!x || !lora_a || !t) return fail(H3Q_ERR_INVALID, "%s: null pointer", who);
-    h3q::GemmArgs g{};
+    g = h3q::GemmArgs{};
     g.a = x;
     g.b = lora_a;
     g.lda = ldx * 2;
@@ -467,7 +465,38 @@ __attribute__((visibility("default"))) int h3q_lora_down(const void* x, int64_t 
     g.k = k;
     g.out = t;
     g.ldo = ldt;
+    return H3Q_OK;
+}
+
+__attribute__((visibility("default"))) int h3q_lora_down(const void* x, int64_t ldx, const void* lora_a,
+                                                         int64_t lda, void* t, int64_t ldt, int64_t m, int64_t k,
+                                                         int64_t rank, void* stream) {
+    const char* who = "h3q_lora_down";
+    h3q::GemmArgs g{};
+    const int rc = lora_down_args(who, x, ldx, lora_a, lda, t, ldt, m, k, rank, g);
+    if (rc != H3Q_OK || m == 0) return rc == H3Q_OK ? ok() : rc;
     return check_launch(h3q::launch_gemm(h3q::kOpBF16, false, g, (hipStream_t)stream), who);
+}
+
+__attribute__((visibility("default"))) int64_t h3q_lora_down_workspace_bytes(int64_t m, int64_t k, int64_t rank) {
+    if (m <= 0 || k <= 0 || rank <= 0) return 0;
+    return h3q::lora_down_workspace_bytes(m, k, rank);
+}
+
+__attribute__((visibility("default"))) int h3q_lora_down_ws(const void* x, int64_t ldx, const void* lora_a,
+                                                            int64_t lda, void* t, int64_t ldt, int64_t m, int64_t k,
+                                                            int64_t rank, void* workspace, int64_t workspace_bytes,
+                                                            void* stream) {
+    const char* who = "h3q_lora_down_ws";
+    h3q::GemmArgs g{};
+    const int rc = lora_down_args(who, x, ldx, lora_a, lda, t, ldt, m, k, rank, g);
+    if (rc != H3Q_OK || m == 0) return rc == H3Q_OK ? ok() : rc;
+    const int64_t need = h3q::lora_down_workspace_bytes(m, k, rank);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return fail(H3Q_ERR_INVALID, "%s: workspace of %lld bytes needed, %lld given", who, (long long)need,
+                    (long long)workspace_bytes);
+    if (need > 0 && !aligned(workspace, 16)) return fail(H3Q_ERR_INVALID, "%s: workspace must be 16-byte aligned", who);
+    return check_launch(h3q::launch_lora_down(g, workspace, workspace_bytes, (hipStream_t)stream), who);
 }
 
 }  // extern "C"

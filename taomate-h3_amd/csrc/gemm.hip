@@ -202,7 +202,7 @@ __device__ __forceinline__ void mma_stage(const H3Q_LDS uint8_t* sa, const H3Q_L
 }
 
 // kEpiScaledF16: the scaled epilogue with binary16 bias and output.
-enum Epi : int { kEpiScaled = 0, kEpiI32 = 1, kEpiBF16 = 2, kEpiScaledF16 = 3 };
+enum Epi : int { kEpiScaled = 0, kEpiI32 = 1, kEpiBF16 = 2, kEpiScaledF16 = 3, kEpiF32 = 4 };
 
 // Wait until the oldest `pending + 1` copy stages of this wave have landed,
 // leaving `pending` younger stages in flight (only used while draining).
@@ -276,12 +276,17 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
     // Main loop.  The steady state always has S - 2 younger stages in flight
     // behind the one it waits for, so its body is branch-free; the last
     // S - 1 k-tiles drain the ring.
-    const int ktiles = (int)((kbytes + BK - 1) / BK);
+    // kEpiF32: blockIdx.y takes k-tiles kt0 .. kt0 + p.kt_split - 1 (a slice
+    // of a split over K) and stores its binary32 partial sums.
+    const int ktiles_all = (int)((kbytes + BK - 1) / BK);
+    const int kt0 = EPI == kEpiF32 ? (int)(blockIdx.y * p.kt_split) : 0;
+    const int ktiles = EPI == kEpiF32 ? (ktiles_all - kt0 < (int)p.kt_split ? ktiles_all - kt0 : (int)p.kt_split)
+                                      : ktiles_all;
     auto issue = [&](int kt, int buf) {
         H3Q_LDS uint8_t* dst = lds + buf * T::STAGE_BYTES;
-        load_tile<T, BM>(ra, dst, (uint32_t)p.lda, (int64_t)kt * BK, kbytes, wave, lane);
+        load_tile<T, BM>(ra, dst, (uint32_t)p.lda, (int64_t)(kt0 + kt) * BK, kbytes, wave, lane);
         if constexpr (TB) load_tile_tiled<T, BN>(rb, dst + BM * BK, steps, kt, nblk, wave, lane);
-        else load_tile<T, BN>(rb, dst + BM * BK, (uint32_t)p.ldb, (int64_t)kt * BK, kbytes, wave, lane);
+        else load_tile<T, BN>(rb, dst + BM * BK, (uint32_t)p.ldb, (int64_t)(kt0 + kt) * BK, kbytes, wave, lane);
     };
 #pragma unroll
     for (int s = 0; s < S - 1; ++s)
@@ -326,9 +331,12 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
     // Epilogue.  Stores go through a buffer resource over this block's output
     // rows, so rows past M fall outside it and are dropped by the hardware;
     // a column group past N is given an out-of-range offset.
-    constexpr uint32_t kEs = EPI == kEpiI32 ? 4 : 2;
+    constexpr uint32_t kEs = EPI == kEpiI32 || EPI == kEpiF32 ? 4 : 2;
     constexpr uint32_t kDrop = 0xFFFFFFF0u;
-    const __amdgpu_buffer_rsrc_t ro = make_rsrc((uint8_t*)p.out + m0 * p.ldo * kEs, (uint32_t)(rows_a * p.ldo * kEs));
+    // kEpiF32: slice blockIdx.y's partial is the [m, ldo] binary32 block y of out.
+    const int64_t slice_row0 = EPI == kEpiF32 ? (int64_t)blockIdx.y * p.m : 0;
+    const __amdgpu_buffer_rsrc_t ro =
+        make_rsrc((uint8_t*)p.out + (slice_row0 + m0) * p.ldo * kEs, (uint32_t)(rows_a * p.ldo * kEs));
     const H3Q_LDS float* sw_l = (const H3Q_LDS float*)lds_sw;
     const H3Q_LDS uint16_t* bias_l = (const H3Q_LDS uint16_t*)lds_bias;
     const bool has_bias = VEC ? BIAS : p.bias != nullptr;
@@ -355,8 +363,14 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_kernel(GemmArgs p, int til
             for (int q = 0; q < 4; ++q) {
                 const int nl = wn0 + 32 * j + 8 * q + 4 * g;  // first of this slot group's 4 columns
                 const int64_t n = n0 + nl;
-                if constexpr (EPI == kEpiI32) {
-                    v4i d = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                if constexpr (EPI == kEpiI32 || EPI == kEpiF32) {
+                    v4i d;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const auto v = acc[i][j][4 * q + e];
+                        if constexpr (EPI == kEpiF32) d[e] = __float_as_int(v);
+                        else d[e] = v;
+                    }
                     if constexpr (VEC) {
                         const uint32_t off = n < p.n ? row_off + (uint32_t)n * kEs : kDrop;
                         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, d), ro, off, 0, 0);
@@ -644,6 +658,72 @@ using TileLora = Tile<128, 128, 128, 4, 2, 2>;
 // K = 5120 60.4-61.5 us against 65.5-66.1; K = 13824 181-188 against
 // 185-186, no change).
 using TileLora96 = Tile<96, 128, 128, 5, 1, 4>;
+
+// Sum of the S binary32 partials of a split LoRA down-projection in slice
+// order, rounded once to bf16: thread (row, 4-column group).
+__global__ __launch_bounds__(256) void lora_down_reduce_kernel(const float* __restrict__ partial, int slices,
+                                                               int64_t m, int rank, uint16_t* __restrict__ t,
+                                                               int64_t ldt) {
+    const int groups = rank / 4;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= m * groups) return;
+    const int64_t row = idx / groups;
+    const int col = (int)(idx % groups) * 4;
+    const v4f* src = reinterpret_cast<const v4f*>(partial + row * rank + col);
+    const int64_t stride = m * rank / 4;  // one slice, in v4f
+    v4f sum = src[0];
+    for (int s = 1; s < slices; ++s) {
+        const v4f v = src[s * stride];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum[e] = sum[e] + v[e];
+    }
+    *reinterpret_cast<v2u*>(t + row * ldt + col) = v2u{pack_out2(sum[0], sum[1], false), pack_out2(sum[2], sum[3], false)};
+}
+
+namespace {
+
+// Slices of the split (1: no split): with fewer than 128 row blocks of 96 the
+// call has too few workgroups to stream X at HBM speed, so K is cut into
+// slices of at least 4 k-tiles until about 256 workgroups run.
+int64_t lora_down_slices(int64_t m, int64_t k, int64_t rank) {
+    const int64_t tiles = (m + TileLora96::BM - 1) / TileLora96::BM;
+    const int64_t ktiles = (k * 2 + TileLora96::BK - 1) / TileLora96::BK;
+    if (tiles >= 128 || rank > TileLora96::BN || rank % 4 || ktiles < 8) return 1;
+    int64_t s = (256 + tiles - 1) / tiles;
+    if (s > ktiles / 4) s = ktiles / 4;
+    const int64_t per = (ktiles + s - 1) / s;
+    return (ktiles + per - 1) / per;  // no empty slice
+}
+
+}  // namespace
+
+int64_t lora_down_workspace_bytes(int64_t m, int64_t k, int64_t rank) {
+    const int64_t s = lora_down_slices(m, k, rank);
+    return s > 1 ? s * m * rank * 4 : 0;
+}
+
+hipError_t launch_lora_down(const GemmArgs& args, void* workspace, int64_t workspace_bytes, hipStream_t st) {
+    const int64_t s = lora_down_slices(args.m, args.k, args.n);
+    // The reduction stores 4 bf16 per lane: t rows 8-byte aligned.
+    const bool t_vec = args.ldo % 4 == 0 && (uintptr_t)args.out % 8 == 0;
+    if (s == 1 || !t_vec || workspace == nullptr || workspace_bytes < s * args.m * args.n * 4)
+        return launch_gemm(kOpBF16, false, args, st);
+    GemmArgs a = args;
+    const int64_t ktiles = (a.k * 2 + TileLora96::BK - 1) / TileLora96::BK;
+    a.kt_split = (ktiles + s - 1) / s;
+    a.out = workspace;
+    a.ldo = a.n;
+    a.out_vec = 1;
+    const int tiles_m = (int)((a.m + TileLora96::BM - 1) / TileLora96::BM);
+    hipLaunchKernelGGL((gemm_kernel<TileLora96, kOpBF16, kEpiF32, false, true, false, false>),
+                       dim3((unsigned)tiles_m, (unsigned)s), dim3(TileLora96::NT), 0, st, a, tiles_m, 1);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t threads = a.m * (a.n / 4);
+    hipLaunchKernelGGL(lora_down_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                       (const float*)workspace, (int)s, a.m, (int)a.n, (uint16_t*)args.out, args.ldo);
+    return hipGetLastError();
+}
 
 hipError_t launch_gemm(int kind, bool raw_i32, const GemmArgs& args, hipStream_t st) {
     GemmArgs a = args;

@@ -85,12 +85,20 @@ struct GemmArgs {
     int out_vec;            // ldo % 4 == 0, n % 4 == 0 and out 16-byte aligned: 4 columns per store
     int a_tiled, b_tiled;   // operand stored in the tiled layout (k % 128 == 0; rows padded to 16 with zeros)
     int out_f16;            // scaled output and bias are IEEE binary16 instead of bf16
+    int64_t kt_split;       // LoRA down-projection split over K: k-tiles per slice (blockIdx.y), 0: no split
 };
 
 // out = epilogue(A @ B^T).  kind: kOpE4M3 / kOpInt8 scaled to bf16 (with
 // optional bias and LoRA); raw_i32: int8 accumulators written as int32;
 // kOpBF16: plain bf16 GEMM (LoRA down-projection).
 hipError_t launch_gemm(int kind, bool raw_i32, const GemmArgs& args, hipStream_t st);
+
+// LoRA down-projection t = bf16(x @ lora_a^T) (kind kOpBF16, n = rank).  With
+// few rows the call is split over K: each slice's binary32 partial goes to
+// the workspace and a second kernel sums the slices in order and rounds.
+// lora_down_workspace_bytes gives the bytes that split needs (0: no split).
+int64_t lora_down_workspace_bytes(int64_t m, int64_t k, int64_t rank);
+hipError_t launch_lora_down(const GemmArgs& args, void* workspace, int64_t workspace_bytes, hipStream_t st);
 
 // Persistent four-wave GEMM for large M (gemm_w4.hip): scaled e4m3 / int8 ->
 // bf16 (or binary16) with optional bias and rank <= 128 LoRA; row-major or

@@ -508,6 +508,14 @@ def lora_down(x: torch.Tensor, lora_a: torch.Tensor, *, out: torch.Tensor | None
     _rows_2d("lora_down out", out, torch.bfloat16)
     if m == 0:
         return out
-    _lib.call("h3q_lora_down", _ptr(x), x.stride(0), _ptr(lora_a), lora_a.stride(0), _ptr(out), out.stride(0), m,
-              k, rank, _stream(x))
+    # Few rows: the library splits K and needs a binary32 workspace for the
+    # slices' partial sums (allocated here, so graph capture keeps it).
+    ws_bytes = int(_lib.lib().h3q_lora_down_workspace_bytes(m, k, rank))
+    if ws_bytes == 0:
+        _lib.call("h3q_lora_down", _ptr(x), x.stride(0), _ptr(lora_a), lora_a.stride(0), _ptr(out), out.stride(0), m,
+                  k, rank, _stream(x))
+        return out
+    ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+    _lib.call("h3q_lora_down_ws", _ptr(x), x.stride(0), _ptr(lora_a), lora_a.stride(0), _ptr(out), out.stride(0), m,
+              k, rank, _ptr(ws), ws_bytes, _stream(x))
     return out

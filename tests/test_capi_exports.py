@@ -22,7 +22,8 @@ def _declared() -> set[str]:
 def test_header_declares_entry_points():
     names = _declared()
     assert {"h3q_quant_rows", "h3q_quant_tensor_e4m3", "h3q_scaled_mm", "h3q_gemm_i8_i32",
-            "h3q_lora_down", "h3q_last_error", "h3q_version", "h3q_tiled_bytes", "h3q_quant_rows_tiled",
+            "h3q_lora_down", "h3q_lora_down_ws", "h3q_lora_down_workspace_bytes", "h3q_last_error", "h3q_version",
+            "h3q_tiled_bytes", "h3q_quant_rows_tiled",
             "h3q_rms_norm_modulate_quant", "h3q_residual_gate_rms_norm_modulate_quant"} <= names
 
 

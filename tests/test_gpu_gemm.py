@@ -303,3 +303,33 @@ def test_tiled_weight_lora_bias_matches_row_major(ops, oracle, device):
     same bits as with row-major weights."""
     out, ref_out, *_ = _tiled_case(ops, oracle, device, 300, 512, 1024, "e4m3", False, bias=True, lora_rank=64)
     np.testing.assert_array_equal(bits16(out), bits16(ref_out))
+
+
+@pytest.mark.parametrize("m,k,rank", [(592, 5376, 128), (3200, 5376, 128), (40, 1024, 64), (257, 2056, 72)])
+def test_lora_down_split_over_k(ops, oracle, device, m, k, rank):
+    """h3q_lora_down_ws splits K for few rows (binary32 partials summed in
+    slice order, one bf16 rounding): within one bf16 rounding of the exact
+    product plus the binary32 accumulation bound, like the unsplit call, and
+    deterministic; a short workspace is refused before any launch."""
+    from taomate_h3_amd import _lib
+    print(f"lora_down split m={m} k={k} rank={rank}", flush=True)
+    gen = torch.Generator().manual_seed(m + k)
+    x = (torch.randn(m, k, generator=gen) * 2.0).to(torch.bfloat16)
+    la = (torch.randn(rank, k, generator=gen) * 0.01).to(torch.bfloat16)
+    need = int(_lib.lib().h3q_lora_down_workspace_bytes(m, k, rank))
+    assert need > 0
+    xg, lag = x.to(device), la.to(device)
+    t = ops.lora_down(xg, lag)
+    t2 = ops.lora_down(xg, lag)
+    torch.cuda.synchronize()
+    assert torch.equal(t, t2)
+    ref = oracle.lora_down_reference(bits16(x), bits16(la))
+    got = oracle.bf16_to_f32(bits16(t)).astype(np.float64)
+    absx = np.abs(oracle.bf16_to_f32(bits16(x)).astype(np.float64))
+    absa = np.abs(oracle.bf16_to_f32(bits16(la)).astype(np.float64))
+    assert np.all(np.abs(got - ref) <= bf16_ulp(ref) + fp32_gemm_bound(k, absx @ absa.T))
+    ws = torch.empty(need - 16, device=device, dtype=torch.uint8)
+    out = torch.empty(m, rank, device=device, dtype=torch.bfloat16)
+    rc = _lib.lib().h3q_lora_down_ws(xg.data_ptr(), k, lag.data_ptr(), k, out.data_ptr(), rank, m, k, rank,
+                                     ws.data_ptr(), need - 16, None)
+    assert rc != 0 and b"workspace" in _lib.lib().h3q_last_error()
