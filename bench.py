@@ -293,6 +293,49 @@ def bench_a6(torch, ops, dev) -> dict:
             "algorithmic_bytes": byts}
 
 
+def bench_h3_lora(torch, ops, dev) -> dict:
+    """The H3 QKV projection with a rank-128 LoRA at a production shape
+    (1088x1920 phase 1: M=3200 tokens, K=5376, N=10752; e4m3 tiled weights and
+    activations): the LoRA down-projection split over K (the path ops.lora_down
+    takes) against the unsplit kernel, then the scaled GEMM with the LoRA
+    epilogue; act-quant + down-projection + GEMM timed inside steps."""
+    from taomate_h3_amd import _lib
+    gen = torch.Generator(device=dev).manual_seed(0)
+    m, k, n = 3200, 5376, 10752
+    x = gpu_randn(torch, (m, k), gen, dev)
+    qw, sw = ops.quant_rows_tiled(gpu_randn(torch, (n, k), gen, dev, 0.02), ops.FMT_E4M3FN)
+    la, lb = gpu_randn(torch, (128, k), gen, dev, 0.01), gpu_randn(torch, (n, 128), gen, dev, 0.01)
+    q_a = torch.empty(m, k, device=dev, dtype=torch.float8_e4m3fn)
+    s_a = torch.empty(m, 1, device=dev, dtype=torch.float32)
+    t = torch.empty(m, 128, device=dev, dtype=torch.bfloat16)
+    y = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+
+    def down_unsplit(_i):
+        _lib.call("h3q_lora_down", x.data_ptr(), k, la.data_ptr(), k, t.data_ptr(), 128, m, k, 128,
+                  torch.cuda.current_stream().cuda_stream)
+
+    def quant(_i):
+        ops.quant_rows_tiled(x, ops.FMT_E4M3FN, codes=q_a, scales=s_a)
+        ops.lora_down(x, la, out=t)
+
+    def gemm(_i):
+        ops.scaled_mm(q_a, qw, s_a.reshape(-1), sw.reshape(-1), lora_t=t, lora_b=lb, lora_scale=1.0, out=y,
+                      a_tiled=True, b_tiled=True, m=m)
+
+    for _ in range(10):
+        quant(0)
+        gemm(0)
+    torch.cuda.synchronize()
+    split_ms = time_events(torch, lambda i: ops.lora_down(x, la, out=t), 16)
+    unsplit_ms = time_events(torch, down_unsplit, 16)
+    q_ms, g_ms = time_in_step(torch, quant, gemm, 8)
+    fl = 2.0 * m * n * k
+    return {"M": m, "N": n, "K": k, "rank": 128, "lora_down_split_us": round(split_ms * 1e3, 1),
+            "lora_down_unsplit_us": round(unsplit_ms * 1e3, 1), "gemm_lora_us": round(g_ms * 1e3, 1),
+            "gemm_fp8_tflops": round(fl / (g_ms * 1e-3) / 1e12, 1),
+            "act_quant_plus_lora_down_us": round(q_ms * 1e3, 1)}
+
+
 def bench_f4(torch, ops, dev) -> dict:
     """Next row (f)4: per-(batch, head) FP8 quantization of one attention
     operand, [1, 8192, 56, 128] bf16 (the FL transformer's 56 heads of 128 at
@@ -581,7 +624,7 @@ def main() -> int:
     del xs, w, q_w, q_a, q_rm, out
     torch.cuda.empty_cache()
     if not args.no_extra:
-        log("secondary configs: c3, c4, c5, f1, f4, a6")
+        log("secondary configs: c3, c4, c5, f1, f4, a6, h3_qkv_lora")
         result["c3"] = bench_c3(torch, ops, dev)
         torch.cuda.empty_cache()
         result["c4"] = bench_c4(torch, ops, dev)
@@ -593,6 +636,8 @@ def main() -> int:
         result["f4"] = bench_f4(torch, ops, dev)
         torch.cuda.empty_cache()
         result["a6"] = bench_a6(torch, ops, dev)
+        torch.cuda.empty_cache()
+        result["h3_qkv_lora"] = bench_h3_lora(torch, ops, dev)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(torch, w_cpu, bias_cpu, x_cpu)
