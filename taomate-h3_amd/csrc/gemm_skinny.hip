@@ -332,12 +332,13 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_tiled_kernel(GemmArgs p) {
     if constexpr (PIPE) {
         // Two register sets: the next chunk's loads are issued before the
         // current chunk's MFMAs (sched_barrier keeps them there, and the
-        // compiler's vmcnt waits then leave the newer chunk in flight).  An
-        // even chunk count issues one chunk of out-of-range loads (zeros, no
-        // memory traffic) past the end.
+        // compiler's vmcnt waits then leave the newer chunk in flight).  The
+        // last one or two chunks are peeled, so no load is issued past the
+        // end and every wait sits in straight-line code.
         v8i wa[SPW][NB], xa[SPW][MT], wb[SPW][NB], xb[SPW][MT];
         load_chunk(0, wa, xa);
-        for (int c = 0; c + 1 < nc; c += 2) {
+        int c = 0;
+        for (; c + 2 < nc; c += 2) {
             load_chunk(c + 1, wb, xb);
             __builtin_amdgcn_sched_barrier(0);
             mfma_chunk(wa, xa);
@@ -345,7 +346,14 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_tiled_kernel(GemmArgs p) {
             __builtin_amdgcn_sched_barrier(0);
             mfma_chunk(wb, xb);
         }
-        if (nc & 1) mfma_chunk(wa, xa);
+        if (c + 1 < nc) {
+            load_chunk(c + 1, wb, xb);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_chunk(wa, xa);
+            mfma_chunk(wb, xb);
+        } else {
+            mfma_chunk(wa, xa);
+        }
     } else {
         // One register set: each chunk's loads, then its MFMAs (one round
         // trip per chunk; with SPW * WAVES >= K / 128 there is one chunk).
@@ -403,12 +411,12 @@ hipError_t launch_tiled_cfg(const GemmArgs& a, hipStream_t st) {
 // activations, 12 rotating weight copies): 32 weight rows per workgroup beat
 // 16 once M >= 64 (each workgroup re-reads all of A from L2, so fewer
 // workgroups move fewer bytes): M = 64 11.6 us vs 15.0 us, M = 128 16.0 us vs
-// 20.5 us; M = 16 7.9 us in one chunk per wave (8.2-9.9 us in two or more,
-// pipelined).  Pipelined single-step chunks: M = 64 11.3 us, M = 128 15.1 us
-// (against 11.6 and 15.8 without).
+// 20.5 us.  Pipelined chunks: M = 64 11.3 us, M = 128 15.1 us with single-step
+// chunks (against 11.6 and 15.8 without); M = 16 7.7 us with two chunks of 5
+// steps (against 7.9 us in one chunk of 10).
 template <int OP, bool A_TILED>
 hipError_t launch_tiled_op(const GemmArgs& a, hipStream_t st) {
-    if (a.m <= 16) return launch_tiled_cfg<OP, 1, 2, 4, 10, false, A_TILED>(a, st);
+    if (a.m <= 16) return launch_tiled_cfg<OP, 1, 2, 4, 5, true, A_TILED>(a, st);
     if (a.m <= 32) return launch_tiled_cfg<OP, 2, 2, 8, 5, false, A_TILED>(a, st);
     if (a.m <= 64) return launch_tiled_cfg<OP, 4, 2, 8, 1, true, A_TILED>(a, st);
     return launch_tiled_cfg<OP, 8, 2, 8, 1, true, A_TILED>(a, st);

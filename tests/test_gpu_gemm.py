@@ -284,7 +284,9 @@ def _tiled_case(ops, oracle, device, m, n, k, fmt, a_tiled, bias, lora_rank=0, s
                                            (300, 512, 1024, False), (640, 768, 5120, False),
                                            (257, 528, 13824, False),
                                            # skinny M > 32: 8 waves split K; 3 and 4 chunks per wave
-                                           (64, 384, 3072, True), (96, 272, 4096, False)])
+                                           (64, 384, 3072, True), (96, 272, 4096, False),
+                                           # skinny M <= 16, 5-step chunks: 6 and 3 chunks per wave
+                                           (16, 256, 13824, True), (8, 264, 7168, False)])
 @pytest.mark.parametrize("fmt", ["e4m3", "int8"])
 def test_tiled_weight_gemm(ops, oracle, device, m, n, k, a_tiled, fmt):
     """Tiled weights (and tiled activations for m <= 128) through the skinny
