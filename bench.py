@@ -127,7 +127,7 @@ def bench_c3(torch, ops, dev) -> dict:
             ops.scaled_mm(q_a, qw, s_a.reshape(-1), sw.reshape(-1), lora_t=t, lora_b=lb, lora_scale=1.0, out=y,
                           a_tiled=True, b_tiled=True, m=m)
 
-        for _ in range(10):  # steady clocks before timing (the headline step is warmed up likewise)
+        for _ in range(30):  # steady clocks before timing (the headline step is warmed up likewise)
             quant(0)
             gemm(0)
         torch.cuda.synchronize()
@@ -322,7 +322,7 @@ def bench_h3_lora(torch, ops, dev) -> dict:
         ops.scaled_mm(q_a, qw, s_a.reshape(-1), sw.reshape(-1), lora_t=t, lora_b=lb, lora_scale=1.0, out=y,
                       a_tiled=True, b_tiled=True, m=m)
 
-    for _ in range(10):
+    for _ in range(60):  # steady clocks before timing (~13 ms of steps)
         quant(0)
         gemm(0)
     torch.cuda.synchronize()
@@ -396,7 +396,7 @@ def bench_c5(torch, ops, dev) -> dict:
     def gemm(_i):
         ops.scaled_mm(q_a, qw, s_a.reshape(-1), sw.reshape(-1), out=y, a_tiled=True, b_tiled=True, m=m)
 
-    for _ in range(10):  # steady clocks before timing
+    for _ in range(30):  # steady clocks before timing (the MFMA clock settles over ~10-30 ms)
         quant(0)
         gemm(0)
     torch.cuda.synchronize()
