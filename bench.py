@@ -441,6 +441,11 @@ def cpu_baseline(torch, w_cpu, bias_cpu, x_cpu, budget_s: float = 12.0) -> dict:
     }
 
 
+# Secondary measurements, in the order they run.
+EXTRAS = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "f1": bench_f1, "f4": bench_f4, "a6": bench_a6,
+          "h3_qkv_lora": bench_h3_lora}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -450,6 +455,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the c3 / c4 / c5 secondary measurements")
+    ap.add_argument("--extra", default=",".join(EXTRAS),
+                    help="comma-separated secondary measurements to run (default: all of %s)" % ",".join(EXTRAS))
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 512 MiB device copy (known bytes) for scaling rocprof "
                          "FETCH_SIZE / WRITE_SIZE counters")
@@ -457,6 +464,11 @@ def main() -> int:
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
+        return 2
+    extras = [] if args.no_extra else [e for e in args.extra.split(",") if e]
+    unknown = [e for e in extras if e not in EXTRAS]
+    if unknown:
+        print(f"bench.py: unknown --extra names {unknown} (known: {list(EXTRAS)})", file=sys.stderr)
         return 2
 
     import torch
@@ -623,21 +635,11 @@ def main() -> int:
     x_cpu, w_cpu, bias_cpu = xs[0].cpu(), w.cpu(), bias.cpu()
     del xs, w, q_w, q_a, q_rm, out
     torch.cuda.empty_cache()
-    if not args.no_extra:
-        log("secondary configs: c3, c4, c5, f1, f4, a6, h3_qkv_lora")
-        result["c3"] = bench_c3(torch, ops, dev)
+    if extras:
+        log("secondary configs: " + ", ".join(extras))
+    for name in extras:
+        result[name] = EXTRAS[name](torch, ops, dev)
         torch.cuda.empty_cache()
-        result["c4"] = bench_c4(torch, ops, dev)
-        torch.cuda.empty_cache()
-        result["c5"] = bench_c5(torch, ops, dev)
-        torch.cuda.empty_cache()
-        result["f1"] = bench_f1(torch, ops, dev)
-        torch.cuda.empty_cache()
-        result["f4"] = bench_f4(torch, ops, dev)
-        torch.cuda.empty_cache()
-        result["a6"] = bench_a6(torch, ops, dev)
-        torch.cuda.empty_cache()
-        result["h3_qkv_lora"] = bench_h3_lora(torch, ops, dev)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(torch, w_cpu, bias_cpu, x_cpu)
