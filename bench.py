@@ -102,12 +102,52 @@ def time_in_step(torch, quant, gemm, iters: int):
     return (sum(e[0].elapsed_time(e[1]) for e in evs) / iters, sum(e[1].elapsed_time(e[2]) for e in evs) / iters)
 
 
+def _c3_lora_module(torch, qw, sw, la, lb):
+    """A column-parallel FP8 W8A8 base (tiled e4m3 weight + per-channel scales,
+    no bias) under the reference's LoRA wrapper, swapped by
+    fuse_h3_lora_wrappers_ for the fused wrapper: the module the c3 object times."""
+    from taomate_h3_amd import ops
+    from taomate_h3_amd.distributed import linear
+    from taomate_h3_amd.inference import lora
+
+    class Base(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.tp_size, self.tp_rank, self.bias = 1, 0, None
+            self.weight = torch.nn.Parameter(qw, requires_grad=False)
+            self.register_buffer("_fp8_w8a8_weight_scale", sw, persistent=False)
+            ops.mark_module_weight_tiled(self)  # as the loaders record a tiled weight
+
+        def forward(self, x):
+            return linear._module_linear(self, x, None)
+
+    # The attributes of the wrapper the reference's apply_h3_lora_checkpoint
+    # installs (H3/inference/lora_checkpoint.py:172-205): what
+    # fuse_h3_lora_wrappers_ reads when it swaps it for this package's.
+    installed = torch.nn.Module()
+    installed.base, installed.kind, installed.scale = Base(), "column", 1.0
+    installed.fused_row_reduce_enabled = False
+    installed._taomate_h3_inference_lora = True
+    installed.register_buffer("lora_a", la, persistent=False)
+    installed.register_buffer("lora_b", lb, persistent=False)
+    root = torch.nn.Module()
+    root.proj = installed.eval()
+    receipt = lora.fuse_h3_lora_wrappers_(root)
+    if receipt["replaced_count"] != 1 or receipt["fused_epilogue_ready_count"] != 1:
+        raise RuntimeError(f"c3: the LoRA wrapper was not swapped for the fused one: {receipt}")
+    return root.proj
+
+
 def bench_c3(torch, ops, dev) -> dict:
     """FFN at 768p, M=24576, up N=13824 K=5120 and down
     N=5120 K=13824, e4m3 per-token x per-channel (activation codes in the
     tiled layout), rank-128 LoRA (scale 1.0) added in the GEMM epilogue.
     Times act-quant + LoRA down + scaled GEMM inside steps (as the headline
-    step), and the GEMM back to back, where the MFMA clock settles lower."""
+    step), and the GEMM back to back, where the MFMA clock settles lower.
+    Then the same linear through the module path a model runs: the
+    reference's LoRA wrapper swapped by fuse_h3_lora_wrappers_, whose forward
+    (LoRA down, tiled act-quant, GEMM with the LoRA epilogue) is timed whole
+    and checked bit for bit against the kernel-level step."""
     gen = torch.Generator(device=dev).manual_seed(0)
     m, out = 24576, {}
     for name, n, k in (("up", 13824, 5120), ("down", 5120, 13824)):
@@ -133,6 +173,9 @@ def bench_c3(torch, ops, dev) -> dict:
         torch.cuda.synchronize()
         q_ms, g_ms = time_in_step(torch, quant, gemm, 8)
         b2b_ms = time_events(torch, gemm, 8)
+        module = _c3_lora_module(torch, qw, sw, la, lb)
+        same = bool(torch.equal(module(x), y))
+        w_ms = time_events(torch, lambda _i: module(x), 8)
         fl = 2.0 * m * n * k
         out[name] = {"M": m, "N": n, "K": k, "gemm_us": round(g_ms * 1e3, 1),
                      "gemm_back_to_back_us": round(b2b_ms * 1e3, 1),
@@ -140,8 +183,10 @@ def bench_c3(torch, ops, dev) -> dict:
                      "pct_fp8_peak": round(100 * fl / (g_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 1),
                      "act_quant_plus_lora_down_us": round(q_ms * 1e3, 1),
                      "step_tflops": round(fl / ((g_ms + q_ms) * 1e-3) / 1e12, 1),
-                     "lora_gflop": round(2.0 * m * 128 * (k + n) / 1e9, 1)}
-        del x, qw, sw, la, lb, q_a, s_a, t, y
+                     "lora_gflop": round(2.0 * m * 128 * (k + n) / 1e9, 1),
+                     "fused_wrapper_forward_us": round(w_ms * 1e3, 1),
+                     "fused_wrapper_matches_kernel_step": same}
+        del x, qw, sw, la, lb, q_a, s_a, t, y, module
     return out
 
 
@@ -441,9 +486,115 @@ def cpu_baseline(torch, w_cpu, bias_cpu, x_cpu, budget_s: float = 12.0) -> dict:
     }
 
 
+def _ceilings_lib():
+    import ctypes
+
+    path = ROOT / "taomate-h3_amd" / "libh3q_ceilings.so"
+    if not path.exists():
+        raise RuntimeError(f"{path.name} is not built: run `python taomate-h3_amd/build.py`")
+    lib = ctypes.CDLL(str(path))
+    P, I64, I = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    for name, args in (("h3q_ceil_read", [P, I64, P, I, P]), ("h3q_ceil_copy", [P, P, I64, I, P]),
+                       ("h3q_ceil_transform", [P, I64, I64, P, I, P]), ("h3q_ceil_mfma", [I, P, I, P, I, P])):
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = I, args
+    return lib
+
+
+def bench_ceilings(torch, ops, dev) -> dict:
+    """Attainable ceilings on this GPU, beside the nominal peaks
+    (taomate-h3_amd/csrc/ceilings.hip, a separate measurement library):
+    * ``hbm_read`` / ``hbm_copy``: stream read of 1 GiB, copy of 512 MiB
+      (read + write bytes), best of three grid sizes;
+    * ``transform``: the per-token quantizer's traffic with no arithmetic
+      (bf16 rows in, one byte per element out, one wavefront per row, a
+      persistent grid), at the c2, c5 and c3-down activation shapes, rotating
+      inputs past the Infinity Cache, best and worst of three grids -- the
+      ceiling of ``act_quant``;
+    * ``mfma_e4m3`` / ``mfma_int8``: the four-wave GEMM's MFMA stream with no
+      memory traffic (one workgroup of four waves per CU, 4 x 4 accumulators
+      of the 32 x 32 MFMA per wave, two fragment sets of bench codes:
+      N(0,1) activations and N(0,0.02) weights quantized per row), at the
+      clock the GPU sustains under it -- the ceiling of ``roofline``."""
+    import ctypes
+
+    lib = _ceilings_lib()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def call(name, *args):
+        rc = getattr(lib, name)(*args, stream)
+        if rc != 0:
+            raise RuntimeError(f"{name} failed ({rc})")
+
+    def p(t):
+        return ctypes.c_void_p(t.data_ptr())
+
+    def best(fn, grids, iters=10):
+        times = {}
+        for g in grids:
+            for i in range(3):
+                fn(g, i)
+            torch.cuda.synchronize()
+            times[g] = time_events(torch, lambda i, g=g: fn(g, i), iters)
+        return times
+
+    res = {"cus": cus}
+    buf = torch.empty(1 << 30, device=dev, dtype=torch.uint8)
+    sink = torch.zeros(64 * cus, device=dev, dtype=torch.int32)
+    grids = (4 * cus, 8 * cus, 16 * cus)
+    t = best(lambda g, _i: call("h3q_ceil_read", p(buf), buf.numel(), p(sink), g), grids)
+    res["hbm_read"] = {"GB/s": round(buf.numel() / (min(t.values()) * 1e-3) / 1e9, 1), "bytes": buf.numel(),
+                       "us_by_grid": {str(g): round(v * 1e3, 1) for g, v in t.items()}}
+    half = buf.numel() // 2
+    src, dst = buf[:half], buf[half:]
+    t = best(lambda g, _i: call("h3q_ceil_copy", p(src), p(dst), half, g), grids)
+    res["hbm_copy"] = {"GB/s": round(2 * half / (min(t.values()) * 1e-3) / 1e9, 1), "bytes_moved": 2 * half,
+                       "us_by_grid": {str(g): round(v * 1e3, 1) for g, v in t.items()}}
+    del buf, src, dst
+    gen = torch.Generator(device=dev).manual_seed(0)
+    res["transform"] = {}
+    for name, m, k, rot in (("c2", 8192, 5120, 4), ("c5", 40960, 5120, 1), ("c3_down", 24576, 13824, 1)):
+        xs = [gpu_randn(torch, (m, k), gen, dev) for _ in range(rot)]
+        out = torch.empty(m, k, device=dev, dtype=torch.uint8)
+        t = best(lambda g, i, xs=xs, out=out, m=m, k=k: call("h3q_ceil_transform", p(xs[i % len(xs)]), m, k, p(out),
+                                                               g), (cus, 4 * cus, 8 * cus), iters=4 * rot)
+        byts = 3 * m * k
+        res["transform"][name] = {"M": m, "K": k, "best_us": round(min(t.values()) * 1e3, 2),
+                                  "worst_us": round(max(t.values()) * 1e3, 2),
+                                  "GB/s": round(byts / (min(t.values()) * 1e-3) / 1e9, 1), "bytes": byts}
+        del xs, out
+    # MFMA stream on bench codes: fragments q < 4 of each set from activation
+    # codes, q >= 4 from weight codes.
+    xq, _ = ops.quant_rows(gpu_randn(torch, (128, 1024), gen, dev), ops.FMT_E4M3FN)
+    wq, _ = ops.quant_rows(gpu_randn(torch, (128, 1024), gen, dev, 0.02), ops.FMT_E4M3FN)
+    frags = torch.cat([xq.view(torch.uint8).reshape(-1, 8, 2048)[:, :4], wq.view(torch.uint8).reshape(-1, 8, 2048)[:, :4]],
+                      dim=1).contiguous()            # [8 (wave, set), 8 fragments, 2048]
+    xi, _ = ops.quant_rows(gpu_randn(torch, (128, 1024), gen, dev), ops.FMT_INT8, ops.ROUND_RCP_MUL)
+    wi, _ = ops.quant_rows(gpu_randn(torch, (128, 1024), gen, dev, 0.02), ops.FMT_INT8)
+    frags_i8 = torch.cat([xi.view(torch.uint8).reshape(-1, 8, 2048)[:, :4],
+                          wi.view(torch.uint8).reshape(-1, 8, 2048)[:, :4]], dim=1).contiguous()
+    if frags.numel() != 128 * 1024 or frags_i8.numel() != 128 * 1024:
+        raise RuntimeError("ceilings: the MFMA stream needs 128 KiB of fragment codes")
+    msink = torch.empty(cus * 256, device=dev, dtype=torch.float32)
+    iters = 2000
+    for name, codes, int8 in (("mfma_e4m3", frags, 0), ("mfma_int8", frags_i8, 1)):
+        def run(_g, _i, codes=codes, int8=int8):
+            call("h3q_ceil_mfma", int8, p(codes), iters, p(msink), cus)
+
+        for _ in range(20):   # about 20 ms of MFMA work: the clock settles under it
+            run(0, 0)
+        torch.cuda.synchronize()
+        ms = time_events(torch, lambda i: run(0, i), 10)
+        flops = cus * 4 * iters * 16 * 131072.0
+        res[name] = {"TFLOP/s" if not int8 else "TOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+                     "us": round(ms * 1e3, 1), "workgroups": cus, "steps_per_wave": iters}
+    return res
+
+
 # Secondary measurements, in the order they run.
 EXTRAS = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "f1": bench_f1, "f4": bench_f4, "a6": bench_a6,
-          "h3_qkv_lora": bench_h3_lora}
+          "h3_qkv_lora": bench_h3_lora, "ceilings": bench_ceilings}
 
 
 def main() -> int:
@@ -542,11 +693,17 @@ def main() -> int:
     torch.cuda.synchronize()
 
     # Timed region: exactly K steps (graph replays) between two synchronisations.
+    # An event after each replay, on the replay stream, gives every step's
+    # device duration (the first from the event before the loop).
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     t0 = time.perf_counter()
+    marks[0].record()
     for i in range(args.steps):
         graphs[i % rotations].replay()
+        marks[i + 1].record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    replay_us = [marks[i].elapsed_time(marks[i + 1]) * 1e3 for i in range(args.steps)]
 
     # Per-kernel durations with HIP events on the launch stream.
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
@@ -597,6 +754,18 @@ def main() -> int:
             "launch": "one HIP graph per step (act-quant + GEMM), replayed",
         },
         "eager_ms_per_step": round(eager_elapsed / args.steps * 1e3, 4),
+        # device time of each timed step (events between the replays, in order):
+        # a falling sequence is the clock still settling, a flat one a fixed cost
+        "step_replay_us": {
+            "min": round(min(replay_us), 1),
+            "median": round(sorted(replay_us)[len(replay_us) // 2], 1),
+            "max": round(max(replay_us), 1),
+            "sum_ms": round(sum(replay_us) / 1e3, 4),
+            "in_order": [round(v, 1) for v in replay_us],
+            # the last quarter of the timed steps: the clock nearest to settled
+            "last_quarter_median": round(sorted(replay_us[-max(1, len(replay_us) // 4):])[
+                max(1, len(replay_us) // 4) // 2], 1),
+        },
         "pct_fp8_peak": round(100.0 * value / FP8_PEAK_TFLOPS, 2),
         "roofline": {
             "kernel": "h3q gemm_w4_kernel (four-wave persistent scaled e4m3 GEMM + dequant + bias epilogue)",
@@ -640,6 +809,16 @@ def main() -> int:
     for name in extras:
         result[name] = EXTRAS[name](torch, ops, dev)
         torch.cuda.empty_cache()
+    ceil = result.get("ceilings")
+    if ceil:
+        # attainable beside nominal: the GEMM against the MFMA stream this GPU
+        # sustains, the act-quant against the plain transform of its traffic
+        att = ceil["mfma_e4m3"]["TFLOP/s"]
+        result["roofline"]["attainable"] = att
+        result["roofline"]["frac_attainable"] = round(result["roofline"]["achieved"] / att, 4)
+        tr = ceil["transform"]["c2"]["GB/s"]
+        result["act_quant"]["attainable"] = tr
+        result["act_quant"]["frac_attainable"] = round(result["act_quant"]["achieved"] / tr, 4)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(torch, w_cpu, bias_cpu, x_cpu)

@@ -84,6 +84,8 @@ def _module_linear(module: nn.Module, inputs: torch.Tensor, bias: torch.Tensor |
     per-token W8A8 paths consume them directly, the others use their bf16 rows."""
     from ..inference.fused_kernels import QuantizedActivations, as_dense
 
+    if getattr(module, ops.TILED_WEIGHT_ATTR, False):
+        ops.module_weight_tiled(module)  # re-marks the storage of a deep-copied tiled weight
     scale = getattr(module, "_cutlass_w8a8_weight_scale", None)
     if isinstance(inputs, QuantizedActivations) and scale is None and \
             getattr(module, "_fp8_w8a8_weight_scale", None) is None:

@@ -148,8 +148,8 @@ def prepare_cutlass_w8a8_stream_load_slot_(torch: Any, module: Any, *, name: str
                                            requires_grad=False)
     elif weight.requires_grad:
         raise RuntimeError(f"{name} preallocated INT8 weight requires gradients")
-    if ops.can_tile(rows, cols) and not ops.is_tiled(module.weight):
-        ops.mark_tiled(module.weight)
+    if ops.can_tile(rows, cols):
+        ops.mark_module_weight_tiled(module)
     module.register_buffer("_cutlass_w8a8_weight_scale",
                            torch.empty((rows, 1), dtype=torch.float32, device=weight.device), persistent=False)
     module._cutlass_w8a8_stream_load_pending = True
@@ -234,6 +234,8 @@ def quantize_h3_interior_qkv_fc1_linears_cutlass_w8a8_(torch: Any, transformer: 
             source_bytes += int(module.weight.numel() * module.weight.element_size())
             parameter, scale = _new_w8_parameter(torch, module.weight)
             module.weight = parameter
+            if ops.is_tiled(parameter):
+                ops.mark_module_weight_tiled(module)
             module.register_buffer("_cutlass_w8a8_weight_scale", scale, persistent=False)
         else:
             source_bytes += int(module._cutlass_w8a8_source_weight_bytes)

@@ -356,7 +356,7 @@ def quantize_h3_block_linears_fp8_w8a8_(torch: Any, transformer: Any, *, policy:
         quantized_bytes += int(quantized.numel() * quantized.element_size())
         module.weight = torch.nn.Parameter(quantized, requires_grad=False)
         if tiled:
-            ops.mark_tiled(module.weight)
+            ops.mark_module_weight_tiled(module)
         module.register_buffer("_fp8_w8a8_weight_scale", scale, persistent=False)
         names.append(name)
     if not names:

@@ -12,7 +12,9 @@ rank is at most 128, this wrapper instead computes t = bf16(x @ A^T) with
 ``h3q_lora_down`` and lets ``h3q_scaled_mm`` add ``scale * t @ B^T`` in the
 GEMM epilogue before the single bf16 rounding of the output.  Other cases
 (a BF16 base, rank above 128) keep the reference's two-GEMM formula.
-Checkpoint loading (lora_checkpoint.py:61-150) is outside this package.
+Checkpoint loading (lora_checkpoint.py:61-150) stays the reference's:
+``fuse_h3_lora_wrappers_`` swaps the wrappers its ``apply_h3_lora_checkpoint``
+installed for this one.
 """
 
 from __future__ import annotations
@@ -33,18 +35,24 @@ class H3LoRACheckpointError(RuntimeError):
     """Raised for adapter shapes or targets the wrapper cannot serve."""
 
 
-def _fusable(base: Any, lora_a: torch.Tensor, lora_b: torch.Tensor) -> bool:
+def _fusable_shape(base: Any, lora_a: torch.Tensor) -> bool:
+    """A W8A8 base (int8 or per-channel FP8) and a rank the GEMM epilogue takes."""
     quantized = (getattr(base, "_cutlass_w8a8_weight_scale", None) is not None
                  or getattr(base, "_fp8_w8a8_weight_scale", None) is not None)
     rank = int(lora_a.shape[0])
-    return (quantized and lora_a.dtype == torch.bfloat16 and lora_b.dtype == torch.bfloat16
-            and 0 < rank <= FUSED_MAX_RANK and rank % 8 == 0 and lora_a.is_cuda)
+    return quantized and 0 < rank <= FUSED_MAX_RANK and rank % 8 == 0 and lora_a.is_cuda
+
+
+def _fusable(base: Any, lora_a: torch.Tensor, lora_b: torch.Tensor) -> bool:
+    return (_fusable_shape(base, lora_a) and lora_a.dtype == torch.bfloat16
+            and lora_b.dtype == torch.bfloat16)
 
 
 def fused_quantized_lora_linear(base: Any, inputs: torch.Tensor, lora_a: torch.Tensor, lora_b: torch.Tensor,
                                 scale: float) -> torch.Tensor:
     """base(x) + scale * (x @ A^T) @ B^T with one bf16 rounding, for a W8A8 base."""
     shape = (*inputs.shape[:-1], int(base.weight.shape[0]))
+    ops.module_weight_tiled(base)  # re-marks the storage of a deep-copied tiled weight
     flat = inputs.reshape(-1, int(inputs.shape[-1]))
     if flat.dtype != torch.bfloat16:
         flat = flat.to(torch.bfloat16)
@@ -69,7 +77,7 @@ def fused_quantized_lora_linear(base: Any, inputs: torch.Tensor, lora_a: torch.T
         w_scale = base._fp8_w8a8_weight_scale
     out = ops.scaled_mm(q, base.weight, s.reshape(-1), w_scale.reshape(-1), bias=bias, lora_t=t,
                         lora_b=lora_b.contiguous(), lora_scale=float(scale), out=out, a_tiled=a_tiled,
-                        b_tiled=ops.is_tiled(base.weight), m=int(flat.shape[0]))
+                        b_tiled=ops.module_weight_tiled(base), m=int(flat.shape[0]))
     return out.reshape(shape)
 
 
@@ -150,6 +158,97 @@ def _adapters(transformer: Any) -> list[tuple[str, Any]]:
             if getattr(module, "_taomate_h3_inference_lora", False)]
 
 
+# The marker attributes the two reference packages set on their wrappers
+# (H3/inference/lora_checkpoint.py:179, FL/inference/lora_checkpoint.py:448);
+# their bf16-materialise, row-reduce, merge and base-model functions find the
+# adapters by these names.
+LORA_WRAPPER_MARKERS = ("_taomate_h3_inference_lora", "_digitalhuman_h3_inference_lora")
+
+
+def _wrapper_markers(module: Any) -> tuple[str, ...]:
+    return tuple(marker for marker in LORA_WRAPPER_MARKERS if getattr(module, marker, False) is True)
+
+
+def fuse_h3_lora_wrappers_(transformer: Any) -> Mapping[str, Any]:
+    """Swap the LoRA wrappers the reference installed for ``H3InferenceParallelLinearLoRA``.
+
+    ``apply_h3_lora_checkpoint`` (H3/inference/lora_checkpoint.py:153-258;
+    FL/inference/lora_checkpoint.py:417-568) builds its wrapper class inside
+    the function and installs one instance per target with ``setattr``
+    (H3 :238-246).  That class computes the base linear and then the two
+    unfused ``F.linear`` calls and elementwise passes.  This function finds
+    every module carrying either package's wrapper marker and replaces it, in
+    its parent, with this package's wrapper holding the same ``base``,
+    ``kind``, ``scale``, ``lora_a`` / ``lora_b`` buffers (the same tensors),
+    ``fused_row_reduce_enabled``, ``adapter_enabled`` and markers, so the
+    reference's later passes (``materialize_h3_lora_bf16_buffers_``,
+    ``enable_h3_fused_lora_row_reduce_``, ``quantize_h3_interior_qkv_fc1_``'s
+    ``getattr(module, "base", module)``) see what they expect.  On a W8A8
+    base with a bf16 adapter of rank <= 128 the forward then adds the LoRA in
+    the GEMM epilogue (checked when the forward runs, so the order against the
+    bf16 materialisation and the W8A8 conversion does not matter).
+
+    A row-parallel wrapper whose base spans several tensor-parallel ranks is
+    left in place: its output needs the cross-rank reduction, which this
+    package does not perform.  Every wrapper is validated before any is
+    replaced; a wrapper that is already this package's is counted, not
+    replaced.  Call it after ``apply_h3_lora_checkpoint`` (H3/runtime/direct.py:116,
+    FL/runtime/direct.py:333) and before the acceleration profile runs."""
+    found = [(name, module) for name, module in transformer.named_modules()
+             if name and _wrapper_markers(module)]
+    if not found:
+        raise H3LoRACheckpointError("fusing LoRA wrappers requires a loaded inference LoRA adapter")
+    plans, already, kept = [], 0, []
+    for name, module in found:
+        if isinstance(module, H3InferenceParallelLinearLoRA):
+            already += 1
+            continue
+        for attr in ("base", "kind", "scale", "lora_a", "lora_b"):
+            if not hasattr(module, attr):
+                raise H3LoRACheckpointError(f"H3 inference LoRA wrapper lacks {attr}: {name}")
+        kind = module.kind
+        if kind not in ("column", "row"):
+            raise H3LoRACheckpointError(f"unknown LoRA target kind {kind}: {name}")
+        base, lora_a, lora_b = module.base, module.lora_a, module.lora_b
+        weight = getattr(base, "weight", None)
+        if weight is None or lora_a.ndim != 2 or lora_b.ndim != 2 or int(lora_a.shape[0]) != int(lora_b.shape[1]):
+            raise H3LoRACheckpointError(f"H3 inference LoRA local shape differs: {name}")
+        if int(lora_a.shape[1]) != int(weight.shape[1]) or int(lora_b.shape[0]) != int(weight.shape[0]):
+            raise H3LoRACheckpointError(f"H3 inference LoRA local shape differs: {name}")
+        if kind == "row" and int(getattr(base, "tp_size", 1)) > 1:
+            kept.append(name)
+            continue
+        plans.append((name, module))
+    fusable = 0
+    for name, module in plans:
+        parent = transformer
+        parts = name.split(".")
+        for part in parts[:-1]:
+            parent = getattr(parent, part)
+        if getattr(parent, parts[-1]) is not module:
+            raise H3LoRACheckpointError(f"H3 inference LoRA target changed: {name}")
+        replacement = H3InferenceParallelLinearLoRA(module.base, kind=module.kind, a=module.lora_a,
+                                                    b=module.lora_b, scale=float(module.scale))
+        replacement.fused_row_reduce_enabled = bool(getattr(module, "fused_row_reduce_enabled", False))
+        replacement.adapter_enabled = bool(getattr(module, "adapter_enabled", True))
+        for marker in _wrapper_markers(module):
+            setattr(replacement, marker, True)
+        replacement.train(module.training)
+        setattr(parent, parts[-1], replacement)
+        if _fusable_shape(replacement.base, replacement.lora_a):
+            fusable += 1
+    return {
+        "schema": "taomate_h3_amd.inference.fused_lora_wrappers.v1",
+        "target_count": len(found),
+        "replaced_count": len(plans),
+        "already_fused_wrapper_count": already,
+        "kept_reference_wrapper_names": kept,
+        # W8A8 bases whose adapter the epilogue takes once its buffers are bf16
+        "fused_epilogue_ready_count": fusable,
+        "fused_max_rank": FUSED_MAX_RANK,
+    }
+
+
 def merge_h3_lora_weights_(transformer: Any) -> Mapping[str, Any]:
     """Fold each loaded adapter into its frozen base weight (FL/inference/lora_checkpoint.py:642-706):
     W' = round_to_base_dtype(fp32(W) + scale * fp32(B) @ fp32(A)), once.  The
@@ -218,5 +317,7 @@ __all__ = [
     "H3LoRACheckpointError",
     "enable_h3_fused_lora_row_reduce_",
     "fused_quantized_lora_linear",
+    "fuse_h3_lora_wrappers_",
+    "LORA_WRAPPER_MARKERS",
     "materialize_h3_lora_bf16_buffers_",
 ]

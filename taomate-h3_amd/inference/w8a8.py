@@ -114,7 +114,7 @@ def prepare_cutlass_w8a8_stream_load_slot_(module: Any, *, name: str) -> None:
     module.weight = torch.nn.Parameter(torch.empty(weight.shape, dtype=torch.int8, device=weight.device),
                                        requires_grad=False)
     if ops.can_tile(int(weight.shape[0]), int(weight.shape[1])):
-        ops.mark_tiled(module.weight)
+        ops.mark_module_weight_tiled(module)
     module.register_buffer("_cutlass_w8a8_weight_scale",
                            torch.empty((int(weight.shape[0]), 1), dtype=torch.float32, device=weight.device),
                            persistent=False)

@@ -173,12 +173,19 @@ def can_tile(rows: int, cols: int) -> bool:
 
 
 # Storages that hold codes in the tiled layout.  The layout is a property of
-# the bytes, so it is recorded against the storage (its device address and
-# size): every view of a marked parameter -- ``weight.t()``, ``.data``,
-# ``.detach()``, slices -- resolves to the same entry, while a copy
-# (``.clone()``, ``.to()``, a new allocation at a reused address of another
-# size) does not.  An entry lives as long as the tensor that was marked.
-_TILED_STORAGES: dict[tuple[str, int, int], int] = {}
+# the bytes, so it is recorded against the storage: every view of a marked
+# parameter -- ``weight.t()``, ``.data``, ``.detach()``, slices -- resolves to
+# the same entry, for as long as any of them keeps the storage alive, while a
+# copy (``.clone()``, ``.to()``, a new allocation at a reused address) does
+# not.  An entry holds a weak reference to the storage object (torch keeps
+# one Python object per live storage) and is dropped when that storage is
+# freed; a lookup also checks that the storage found is the one recorded.
+_TILED_STORAGES: dict[tuple[str, int, int], weakref.ref] = {}
+
+# Module attribute set when this package stores the module's weight tiled.  A
+# ``copy.deepcopy`` of the module copies the attribute with new, unmarked
+# storage; ``module_weight_tiled`` re-marks such a copy.
+TILED_WEIGHT_ATTR = "_h3q_tiled_weight"
 
 
 def _storage_key(t: torch.Tensor) -> tuple[str, int, int]:
@@ -186,19 +193,17 @@ def _storage_key(t: torch.Tensor) -> tuple[str, int, int]:
     return (str(t.device), int(st.data_ptr()), int(st.nbytes()))
 
 
-def _unmark(key: tuple[str, int, int]) -> None:
-    count = _TILED_STORAGES.get(key, 0) - 1
-    if count > 0:
-        _TILED_STORAGES[key] = count
-    else:
-        _TILED_STORAGES.pop(key, None)
+def _unmark(key: tuple[str, int, int], ref: weakref.ref) -> None:
+    if _TILED_STORAGES.get(key) is ref:
+        del _TILED_STORAGES[key]
 
 
 def is_tiled(t: torch.Tensor | None) -> bool:
     """True when ``t`` (or any view of the same storage) holds tiled codes."""
     if t is None or not isinstance(t, torch.Tensor) or t.device.type == "meta":
         return False
-    return _storage_key(t) in _TILED_STORAGES
+    ref = _TILED_STORAGES.get(_storage_key(t))
+    return ref is not None and ref() is t.untyped_storage()
 
 
 def mark_tiled(t: torch.Tensor) -> torch.Tensor:
@@ -206,10 +211,43 @@ def mark_tiled(t: torch.Tensor) -> torch.Tensor:
     (``t`` must cover its whole storage, as a freshly allocated weight does)."""
     if t.data_ptr() != t.untyped_storage().data_ptr() or t.numel() * t.element_size() != t.untyped_storage().nbytes():
         raise ValueError("mark_tiled: the tensor must cover its whole storage")
+    if is_tiled(t):
+        return t
+    storage = t.untyped_storage()
     key = _storage_key(t)
-    _TILED_STORAGES[key] = _TILED_STORAGES.get(key, 0) + 1
-    weakref.finalize(t, _unmark, key)
+    ref = weakref.ref(storage)
+    _TILED_STORAGES[key] = ref
+    weakref.finalize(storage, _unmark, key, ref)
     return t
+
+
+def mark_module_weight_tiled(module: torch.nn.Module) -> torch.Tensor:
+    """Mark ``module.weight``'s storage tiled and record the layout on the module."""
+    mark_tiled(module.weight)
+    setattr(module, TILED_WEIGHT_ATTR, True)
+    return module.weight
+
+
+def module_weight_tiled(module: torch.nn.Module) -> bool:
+    """Whether ``module.weight`` holds tiled codes.  A weight whose module
+    records the tiled layout but whose storage is unmarked is a copy of the
+    tiled bytes (``copy.deepcopy`` of the module): its storage is marked
+    here, so the copy computes what the original does.  deepcopy clones a
+    parameter apart from the tensors that viewed it, so a precomputed
+    ``_cutlass_w8a8_weight_t`` (H3/inference/w8a8.py:283) that no longer
+    views the weight's storage is replaced by ``weight.t()``."""
+    weight = getattr(module, "weight", None)
+    if not is_tiled(weight):
+        if not getattr(module, TILED_WEIGHT_ATTR, False) or not isinstance(weight, torch.Tensor):
+            return False
+        rows, cols = (int(v) for v in weight.shape) if weight.ndim == 2 else (0, 0)
+        if weight.dtype not in (torch.int8, torch.float8_e4m3fn) or not can_tile(rows, cols):
+            raise ValueError("the module records a tiled weight, but its weight is not a tiled code matrix")
+        mark_tiled(weight)
+    weight_t = getattr(module, "_cutlass_w8a8_weight_t", None)
+    if isinstance(weight_t, torch.Tensor) and not is_tiled(weight_t):
+        module._cutlass_w8a8_weight_t = weight.t()
+    return True
 
 
 def check_layout(name: str, t: torch.Tensor, tiled: bool) -> None:

@@ -73,3 +73,54 @@ class ToyRowLinear(torch.nn.Module):
     def forward(self, inputs: torch.Tensor) -> torch.Tensor:
         out = self.reduce_local_output(self.forward_local(inputs))
         return out if self.bias is None else out + self.bias
+
+
+class ToyReferenceLoRAWrapper(torch.nn.Module):
+    """Stand-in for the wrapper class that the reference's
+    ``apply_h3_lora_checkpoint`` defines inside the function and installs with
+    ``setattr`` (H3/inference/lora_checkpoint.py:172-205, FL :440-489): the
+    same attribute names, marker and buffers, and the same unfused forward
+    (base, then two ``F.linear`` calls and the scaled add), single rank only."""
+
+    def __init__(self, base, *, kind: str, a: torch.Tensor, b: torch.Tensor, scale: float,
+                 marker: str = "_taomate_h3_inference_lora") -> None:
+        super().__init__()
+        self.base = base
+        self.kind = kind
+        self.scale = scale
+        self.fused_row_reduce_enabled = False
+        if marker == "_digitalhuman_h3_inference_lora":
+            self.adapter_enabled = True
+        setattr(self, marker, True)
+        self.register_buffer("lora_a", a, persistent=False)
+        self.register_buffer("lora_b", b, persistent=False)
+
+    def forward(self, inputs: torch.Tensor) -> torch.Tensor:
+        output = self.base(inputs)
+        if not getattr(self, "adapter_enabled", True):
+            return output
+        compute_dtype = output.dtype
+        update = torch.nn.functional.linear(
+            torch.nn.functional.linear(inputs.to(compute_dtype), self.lora_a.to(compute_dtype)),
+            self.lora_b.to(compute_dtype))
+        return output + update * self.scale
+
+
+def install_reference_lora(transformer: torch.nn.Module, targets, *, rank: int, scale: float, seed: int,
+                           marker: str = "_taomate_h3_inference_lora") -> dict:
+    """Install ToyReferenceLoRAWrapper on each named target the way the
+    reference does (fp32 A [rank, K_local] and B [N_local, rank] buffers on the
+    weight's device, then ``setattr`` on the parent); returns the wrappers."""
+    gen = torch.Generator().manual_seed(seed)
+    installed = {}
+    for name in targets:
+        module = transformer.get_submodule(name)
+        n, k = (int(v) for v in module.weight.shape)
+        kind = "row" if hasattr(module, "local_input_size") else "column"
+        a = (torch.randn(rank, k, generator=gen) * 0.02).to(module.weight.device)
+        b = (torch.randn(n, rank, generator=gen) * 0.02).to(module.weight.device)
+        wrapper = ToyReferenceLoRAWrapper(module, kind=kind, a=a, b=b, scale=scale, marker=marker).eval()
+        parent_name, _, leaf = name.rpartition(".")
+        setattr(transformer.get_submodule(parent_name) if parent_name else transformer, leaf, wrapper)
+        installed[name] = wrapper
+    return installed

@@ -29,4 +29,4 @@ def test_secondary_measurements_are_listed_in_run_order():
         import bench
     finally:
         sys.path.remove(str(ROOT))
-    assert list(bench.EXTRAS) == ["c3", "c4", "c5", "f1", "f4", "a6", "h3_qkv_lora"]
+    assert list(bench.EXTRAS) == ["c3", "c4", "c5", "f1", "f4", "a6", "h3_qkv_lora", "ceilings"]

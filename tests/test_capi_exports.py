@@ -161,3 +161,12 @@ def test_per_head_quant_errors_without_gpu():
     assert lib.h3q_quant_per_head_workspace_floats(4, 65536, 8, 128) == 4 * 8 * 512
     assert lib.h3q_quant_per_head_workspace_floats(2, 3, 4096, 8) == 2 * 4096 * 8
     assert lib.h3q_quant_per_head_workspace_floats(1, 5, 3, 128) == 3
+
+
+def test_ceilings_library_exports_measurement_entry_points():
+    """bench.py's ceilings object loads its own measurement library (not the
+    product's C ABI); it must be built and export its four entry points."""
+    path = ROOT / "taomate-h3_amd" / "libh3q_ceilings.so"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True).stdout
+    names = set(re.findall(r"\bT (h3q_\w+)", out))
+    assert names == {"h3q_ceil_read", "h3q_ceil_copy", "h3q_ceil_transform", "h3q_ceil_mfma"}

@@ -25,7 +25,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import activations, bf16_ulp, bits16, bits8, weights
+from _util import activations, bf16_ulp, bits16, bits8, from_tiled, weights
 from test_gpu_gemm import _assert_fp8_close
 
 pytestmark = pytest.mark.gpu
@@ -98,15 +98,17 @@ def test_c2_row_major_and_tiled_layouts_agree(ops, device):
         np.testing.assert_array_equal(bits16(o), ref)
 
 
+@pytest.mark.parametrize("a_tiled", [False, True])
 @pytest.mark.parametrize("which", ["up", "down"])
-def test_c3_ffn_lora_stratified(ops, oracle, device, which):
+def test_c3_ffn_lora_stratified(ops, oracle, device, which, a_tiled):
     """c3 (768p FFN, M=24576): up N=13824 K=5120 and down N=5120 K=13824,
     e4m3 tiled weights, rank-128 bf16 LoRA with alpha=128 (scale 1.0) in the
-    GEMM epilogue."""
+    GEMM epilogue; row-major activation codes, and the tiled ones the bench
+    times."""
     m = 24576
     n, k = (13824, 5120) if which == "up" else (5120, 13824)
     rank = 128
-    print(f"c3 {which}: {m}x{n}x{k} LoRA rank {rank}", flush=True)
+    print(f"c3 {which}: {m}x{n}x{k} LoRA rank {rank} a_tiled={a_tiled}", flush=True)
     x = activations(m, k, seed=7, outlier_channels=0)
     w = weights(n, k, seed=8)
     gen = torch.Generator().manual_seed(9)
@@ -114,10 +116,11 @@ def test_c3_ffn_lora_stratified(ops, oracle, device, which):
     lb = (torch.randn(n, rank, generator=gen) * 0.01).to(torch.bfloat16)
     xg = x.to(device)
     qw, sw = _quant_weights(ops, w, device, "e4m3")
-    qa, sa = ops.quant_rows(xg, ops.FMT_E4M3FN)
+    quant = ops.quant_rows_tiled if a_tiled else ops.quant_rows
+    qa, sa = quant(xg, ops.FMT_E4M3FN)
     t = ops.lora_down(xg, la.to(device))
     out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), lora_t=t, lora_b=lb.to(device), lora_scale=1.0,
-                        b_tiled=True, n=n)
+                        a_tiled=a_tiled, b_tiled=True, m=m, n=n)
     torch.cuda.synchronize()
     rows = stratified_rows(m, seed=1)
     xr = bits16(x[torch.from_numpy(rows)])
@@ -156,23 +159,28 @@ def test_c3_ffn_lora_stratified(ops, oracle, device, which):
     assert np.mean(err <= bf16_ulp(np.abs(ref))) >= 0.99
 
 
-def test_c5_int8_full_size_bit_exact(ops, oracle, device):
+@pytest.mark.parametrize("a_tiled", [False, True])
+def test_c5_int8_full_size_bit_exact(ops, oracle, device, a_tiled):
     """c5 (1080p, M=40960, K=N=5120, int8 with Student-t outlier channels):
-    per-token vLLM-form activation codes, per-channel weight codes (tiled),
-    bf16 outputs bit-exact on the stratified rows; int32 accumulators
-    bit-exact on the same rows."""
+    per-token vLLM-form activation codes (row-major, and tiled as the bench
+    times them), per-channel weight codes (tiled), bf16 outputs bit-exact on
+    the stratified rows; int32 accumulators bit-exact on the same rows."""
     m, k, n = 40960, 5120, 5120
-    print("c5 int8 full size", flush=True)
+    print(f"c5 int8 full size a_tiled={a_tiled}", flush=True)
     x = activations(m, k, seed=11, outlier_channels=k // 100, student_t=True)
     w = weights(n, k, seed=12)
     xg = x.to(device)
     qw, sw = _quant_weights(ops, w, device, "int8")
-    qa, sa = ops.quant_rows(xg, ops.FMT_INT8, ops.ROUND_RCP_MUL)
-    out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), b_tiled=True, n=n)
+    quant = ops.quant_rows_tiled if a_tiled else ops.quant_rows
+    qa, sa = quant(xg, ops.FMT_INT8, ops.ROUND_RCP_MUL)
+    out = ops.scaled_mm(qa, qw, sa.reshape(-1), sw.reshape(-1), a_tiled=a_tiled, b_tiled=True, m=m, n=n)
     torch.cuda.synchronize()
     rows = stratified_rows(m, seed=2)
     rqa, rsa = oracle.quant_rows(bits16(x[torch.from_numpy(rows)]), "int8", "rcp")
-    np.testing.assert_array_equal(bits8(qa)[rows], rqa.view(np.uint8))
+    codes = from_tiled(bits8(qa), m, k) if a_tiled else bits8(qa)
+    np.testing.assert_array_equal(codes[rows], rqa.view(np.uint8))
+    if a_tiled:
+        qa = ops.quant_rows(xg, ops.FMT_INT8, ops.ROUND_RCP_MUL)[0]  # row-major rows for the i32 entry point
     rqw, rsw = oracle.quant_rows(bits16(w), "int8", "div")
     acc = oracle.gemm_i8_i32(rqa, rqw)
     np.testing.assert_array_equal(bits16(out)[rows], oracle.epilogue(acc, rsa, rsw))

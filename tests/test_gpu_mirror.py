@@ -412,3 +412,75 @@ def test_lora_adapter_switch_on_a_quantized_base(device):
     torch.cuda.synchronize()
     assert torch.equal(without, base(x))
     assert not torch.equal(with_adapter, without)
+
+
+@pytest.mark.parametrize("scale", [1.0, 0.75])
+@pytest.mark.parametrize("tokens", [(2, 150), (1, 96)])
+def test_reference_lora_wrappers_swapped_to_fused_epilogue(oracle, device, monkeypatch, scale, tokens):
+    """The drop-in path of the LoRA epilogue: wrappers shaped like the ones the
+    reference's apply_h3_lora_checkpoint installs (H3/inference/lora_checkpoint.py:
+    172-246; fp32 buffers) on int8 W8A8 bases (FL/inference/w8a8.py:340-466
+    post-load conversion through ``getattr(module, "base", module)``), bf16
+    buffers materialised (:261-284), then fuse_h3_lora_wrappers_.  The swapped
+    wrappers on W8A8 bases take the fused GEMM epilogue and agree with the
+    reference's three rounding points (:196-205) to 4 bf16 ulps; the one on a
+    bf16 base keeps the reference's formula bit for bit."""
+    from _toy_layers import install_reference_lora
+
+    fl = _mod("inference.fl_w8a8")
+    lora = _mod("inference.lora")
+    model = _Transformer(device=device)
+    targets = ["blocks.2.attn.qkv_proj", "blocks.3.mlp.fc1", "blocks.0.attn.qkv_proj"]
+    installed = install_reference_lora(model, targets, rank=128, scale=scale, seed=61)
+    fl.quantize_h3_interior_qkv_fc1_linears_cutlass_w8a8_(torch, model, policy="interior_fc1_qkv_v1")
+    lora.materialize_h3_lora_bf16_buffers_(model)
+    x = activations(tokens[0] * tokens[1], 256, seed=62, outlier_channels=2).reshape(*tokens, 256).to(device)
+    before = {name: installed[name](x) for name in targets}
+    receipt = lora.fuse_h3_lora_wrappers_(model)
+    assert receipt["replaced_count"] == 3 and receipt["fused_epilogue_ready_count"] == 2
+    calls = []
+    fused = lora.fused_quantized_lora_linear
+    monkeypatch.setattr(lora, "fused_quantized_lora_linear", lambda *a: calls.append(1) or fused(*a))
+    after = {name: model.get_submodule(name)(x) for name in targets}
+    torch.cuda.synchronize()
+    assert len(calls) == 2
+    from _util import bf16_ulp
+
+    flat = bits16(x.reshape(-1, 256))
+    for name in targets[:2]:
+        wrapper = model.get_submodule(name)
+        assert isinstance(wrapper, lora.H3InferenceParallelLinearLoRA)
+        assert wrapper.lora_a is installed[name].lora_a and wrapper.lora_a.dtype == torch.bfloat16
+        n = int(wrapper.base.weight.shape[0])
+        base_out = bits16(wrapper.base(x).reshape(-1, n))
+        ref = oracle.bf16_to_f32(oracle.lora_reference(flat, bits16(wrapper.lora_a), bits16(wrapper.lora_b), scale,
+                                                       base_out)).astype(np.float64)
+        base_f = oracle.bf16_to_f32(base_out).astype(np.float64)
+        # one rounding against three: 4 ulps of the largest of output, base and update
+        bound = 4 * bf16_ulp(np.maximum(np.maximum(np.abs(ref), np.abs(base_f)), np.abs(ref - base_f)))
+        for got_t in (after[name], before[name]):
+            got = oracle.bf16_to_f32(bits16(got_t.reshape(-1, n))).astype(np.float64)
+            assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 2.0 ** -7
+            assert np.all(np.abs(got - ref) <= bound)
+    assert torch.equal(after[targets[2]], before[targets[2]])
+
+
+def test_deepcopy_of_a_tiled_w8a8_model(device):
+    """copy.deepcopy of a model whose W8 weights are stored tiled (FL's
+    post-load conversion, then the workspace with its precomputed weight_t
+    views): the copy's projections return the original's bits."""
+    import copy
+
+    fl = _mod("inference.fl_w8a8")
+    model = _Transformer(device=device)
+    fl.quantize_h3_interior_qkv_fc1_linears_cutlass_w8a8_(torch, model, policy="interior_fc1_qkv_v1")
+    fl.enable_h3_cutlass_w8a8_workspace_(torch, model)
+    twin = copy.deepcopy(model)
+    for rows in (300, 64):
+        x = activations(rows, 256, seed=63 + rows, outlier_channels=2).to(device)
+        for name in ("blocks.2.attn.qkv_proj", "blocks.3.mlp.fc1"):
+            ref = model.get_submodule(name)(x).clone()
+            got = twin.get_submodule(name)(x)
+            torch.cuda.synchronize()
+            assert torch.equal(got, ref), name
+    assert ops_mod.is_tiled(twin.get_submodule("blocks.3.mlp.fc1").weight)

@@ -209,6 +209,80 @@ def test_lora_merge_and_base_model_bypass():
             pass
 
 
+def _lora_toy_model(tp=(1, 0)):
+    from _toy_layers import ToyColumnLinear, ToyRowLinear
+
+    root = torch.nn.Module()
+    root.blocks = torch.nn.ModuleList()
+    for _ in range(2):
+        block = torch.nn.Module()
+        block.attn = torch.nn.Module()
+        block.attn.qkv_proj = ToyColumnLinear(32, 96, bias=False, dtype=torch.bfloat16, tp=tp)
+        block.attn.out_proj = ToyRowLinear(32, 32, bias=True, dtype=torch.bfloat16, tp=tp)
+        root.blocks.append(block)
+    return root
+
+
+@pytest.mark.parametrize("marker", ["_taomate_h3_inference_lora", "_digitalhuman_h3_inference_lora"])
+def test_fuse_lora_wrappers_swaps_reference_wrappers(marker):
+    """fuse_h3_lora_wrappers_ replaces the wrappers the reference's
+    apply_h3_lora_checkpoint installs (H3/inference/lora_checkpoint.py:172-246,
+    FL :440-553) in their parents, keeping base, kind, scale, the same buffer
+    tensors, the row-reduce and adapter switches and the package's marker."""
+    from _toy_layers import install_reference_lora
+    from taomate_h3_amd.inference import lora
+
+    root = _lora_toy_model()
+    names = ["blocks.0.attn.qkv_proj", "blocks.0.attn.out_proj", "blocks.1.attn.qkv_proj"]
+    installed = install_reference_lora(root, names, rank=8, scale=0.5, seed=3, marker=marker)
+    installed["blocks.0.attn.out_proj"].fused_row_reduce_enabled = True
+    if marker == "_digitalhuman_h3_inference_lora":
+        installed["blocks.1.attn.qkv_proj"].adapter_enabled = False
+    receipt = lora.fuse_h3_lora_wrappers_(root)
+    assert receipt["target_count"] == 3 and receipt["replaced_count"] == 3
+    assert receipt["already_fused_wrapper_count"] == 0 and receipt["kept_reference_wrapper_names"] == []
+    assert receipt["fused_epilogue_ready_count"] == 0  # bf16 toy bases, not W8A8
+    for name, old in installed.items():
+        new = root.get_submodule(name)
+        assert isinstance(new, lora.H3InferenceParallelLinearLoRA)
+        assert new.base is old.base and new.kind == old.kind and new.scale == old.scale
+        assert new.lora_a is old.lora_a and new.lora_b is old.lora_b
+        assert getattr(new, marker) is True and new._taomate_h3_inference_lora is True
+        assert new.fused_row_reduce_enabled == old.fused_row_reduce_enabled
+        assert new.adapter_enabled == getattr(old, "adapter_enabled", True)
+        assert not new.training
+    # the reference's later passes still find the adapters; a second swap replaces nothing
+    assert lora.materialize_h3_lora_bf16_buffers_(root)["target_count"] == 3
+    again = lora.fuse_h3_lora_wrappers_(root)
+    assert again["replaced_count"] == 0 and again["already_fused_wrapper_count"] == 3
+
+
+def test_fuse_lora_wrappers_validates_before_replacing():
+    """A wrapper whose buffers do not fit its base fails the whole call before
+    any wrapper is replaced; a model without adapters raises; a row-parallel
+    wrapper over several ranks stays the reference's (it needs the cross-rank
+    reduce)."""
+    from _toy_layers import ToyReferenceLoRAWrapper, install_reference_lora
+    from taomate_h3_amd.inference import lora
+
+    with pytest.raises(lora.H3LoRACheckpointError, match="requires a loaded inference LoRA adapter"):
+        lora.fuse_h3_lora_wrappers_(_lora_toy_model())
+    root = _lora_toy_model()
+    install_reference_lora(root, ["blocks.0.attn.qkv_proj"], rank=8, scale=1.0, seed=4)
+    bad_base = root.blocks[1].attn.qkv_proj
+    root.blocks[1].attn.qkv_proj = ToyReferenceLoRAWrapper(bad_base, kind="column", a=torch.zeros(8, 31),
+                                                           b=torch.zeros(96, 8), scale=1.0)
+    with pytest.raises(lora.H3LoRACheckpointError, match="local shape differs: blocks.1.attn.qkv_proj"):
+        lora.fuse_h3_lora_wrappers_(root)
+    assert not isinstance(root.blocks[0].attn.qkv_proj, lora.H3InferenceParallelLinearLoRA)
+    split = _lora_toy_model(tp=(2, 0))
+    install_reference_lora(split, ["blocks.0.attn.qkv_proj", "blocks.0.attn.out_proj"], rank=8, scale=1.0, seed=5)
+    receipt = lora.fuse_h3_lora_wrappers_(split)
+    assert receipt["replaced_count"] == 1 and receipt["kept_reference_wrapper_names"] == ["blocks.0.attn.out_proj"]
+    assert isinstance(split.blocks[0].attn.qkv_proj, lora.H3InferenceParallelLinearLoRA)
+    assert not isinstance(split.blocks[0].attn.out_proj, lora.H3InferenceParallelLinearLoRA)
+
+
 def test_ops_reject_host_tensors_before_launch():
     x = torch.zeros(4, 16, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
@@ -255,3 +329,50 @@ def test_fused_norm_mirrors_check_indices_and_devices():
     qa = fk.QuantizedActivations(torch.zeros(6, 16, dtype=torch.int8), torch.ones(6, 1), (2, 3, 16))
     with pytest.raises(TypeError, match="keep_dense=True"):
         fk.as_dense(qa)
+
+
+def test_tiled_mark_lives_with_the_storage():
+    """The tiled mark belongs to the storage: a view that outlives the marked
+    parameter still reads as tiled; the entry goes when the last view goes;
+    a copy is not tiled."""
+    import gc
+
+    param = torch.nn.Parameter(torch.zeros(32, 256, dtype=torch.int8), requires_grad=False)
+    ops.mark_tiled(param)
+    view = param.t()
+    key = ops._storage_key(param)
+    assert ops.is_tiled(view) and ops.is_tiled(param.data) and ops.is_tiled(param.detach()[:16])
+    assert not ops.is_tiled(param.detach().clone())
+    del param
+    gc.collect()
+    assert ops.is_tiled(view) and key in ops._TILED_STORAGES
+    del view
+    gc.collect()
+    assert key not in ops._TILED_STORAGES
+    with pytest.raises(ValueError, match="whole storage"):
+        ops.mark_tiled(torch.zeros(32, 256, dtype=torch.int8)[:16])
+
+
+def test_tiled_weight_survives_deepcopy_of_its_module():
+    """copy.deepcopy of a module whose weight this package stored tiled gives
+    new, unmarked storage; the module records the layout, and the dispatch
+    re-marks the copy (ops.module_weight_tiled), so the copy computes what the
+    original does.  The weight_t view copied beside it resolves to the same storage."""
+    import copy
+
+    m = torch.nn.Module()
+    m.weight = torch.nn.Parameter(torch.zeros(32, 256, dtype=torch.int8), requires_grad=False)
+    ops.mark_module_weight_tiled(m)
+    m._cutlass_w8a8_weight_t = m.weight.t()
+    twin = copy.deepcopy(m)
+    assert twin.weight.untyped_storage().data_ptr() != m.weight.untyped_storage().data_ptr()
+    assert not ops.is_tiled(twin.weight) and not ops.is_tiled(twin._cutlass_w8a8_weight_t)
+    assert ops.module_weight_tiled(twin)
+    assert ops.is_tiled(twin.weight) and ops.is_tiled(twin._cutlass_w8a8_weight_t)
+    assert ops.module_weight_tiled(m)
+    plain = torch.nn.Module()
+    plain.weight = torch.nn.Parameter(torch.zeros(32, 256, dtype=torch.int8), requires_grad=False)
+    assert not ops.module_weight_tiled(plain)
+    twin.weight = torch.nn.Parameter(torch.zeros(30, 256, dtype=torch.int8), requires_grad=False)
+    with pytest.raises(ValueError, match="not a tiled code matrix"):
+        ops.module_weight_tiled(twin)

@@ -24,6 +24,11 @@ def _p(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def _device_memory(device):
+    return (torch.cuda.memory_allocated(device), torch.cuda.memory_reserved(device),
+            torch.cuda.mem_get_info(device)[0])
+
+
 def _run(lib, name, x, static=None):
     rows, cols = x.shape
     codes = torch.empty((rows, cols), device=x.device, dtype=torch.float8_e4m3fn)
@@ -35,10 +40,14 @@ def _run(lib, name, x, static=None):
         rc = lib.h3q_quant_tensor_e4m3(_p(x), rows, cols, x.stride(0), _p(static), _p(ws), _p(codes), cols,
                                        _p(scale), stream)
     else:
-        before = torch.cuda.memory_allocated(x.device)
+        torch.cuda.synchronize()
+        before = _device_memory(x.device)
         rc = lib.h3q_quant_tensor_e4m3_noalloc(_p(x), rows, cols, x.stride(0), _p(static), _p(codes), cols,
                                                _p(scale), stream)
-        assert torch.cuda.memory_allocated(x.device) == before
+        torch.cuda.synchronize()
+        # torch's allocator counters, and the device's free memory, which a
+        # hipMalloc inside the library would lower
+        assert _device_memory(x.device) == before
     assert rc == 0, lib.h3q_last_error()
     torch.cuda.synchronize()
     return bits8(codes), scale.cpu().numpy()
