@@ -594,6 +594,74 @@ def bench_ceilings(torch, ops, dev) -> dict:
     return res
 
 
+def cpu_baseline_per_config(torch, budget_s: float = 1.0) -> dict:
+    """The reference's formulas on the host (oracle/torch_path.py) for each
+    BASELINE config, on a bounded row sample (synthetic inputs of the config's
+    shape and distribution): act-quant (3MK + 4M bytes), the quantized GEMM
+    (2MNK; FP8 dequant-then-matmul, which dequantizes the weight every call as
+    that path does, int8 torch._int_mm then the epilogue), LoRA (c3) and the
+    end-to-end time scaled to the config's full M.  Median of at least 3 runs
+    per piece, about budget_s seconds each (about 20 s in all on 8 cores)."""
+    from oracle import torch_path as TP
+    import torch.nn.functional as F
+
+    gen = torch.Generator().manual_seed(0)
+
+    def med(fn):
+        times, t_start = [], time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 15):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return sorted(times)[len(times) // 2]
+
+    out = {}
+    cases = (("c1", 256, 1024, 1024, 256, "e4m3", 8, 20.0, False, True),
+             ("c3_up", 24576, 5120, 13824, 512, "e4m3", 0, 0.0, True, False),
+             ("c3_down", 24576, 13824, 5120, 256, "e4m3", 0, 0.0, True, False),
+             ("c4_M16", 16, 5120, 5120, 16, "e4m3", 0, 0.0, False, False),
+             ("c4_M64", 64, 5120, 5120, 64, "e4m3", 0, 0.0, False, False),
+             ("c4_M128", 128, 5120, 5120, 128, "e4m3", 0, 0.0, False, False),
+             ("c5", 40960, 5120, 5120, 512, "int8", 51, 0.0, False, False))
+    for name, m, k, n, rows, fmt, outl, oscale, lora, bias in cases:
+        x = torch.randn(rows, k, generator=gen)
+        if outl:
+            idx = torch.randperm(k, generator=gen)[:outl]
+            if fmt == "int8":   # heavy-tailed Student-t(3) channels
+                chi = torch.distributions.Chi2(torch.full((outl,), 3.0)).sample((rows,))
+                x[:, idx] = torch.randn(rows, outl, generator=gen) / torch.sqrt(chi / 3.0)
+            else:
+                x[:, idx] *= oscale
+        x = x.to(torch.bfloat16)
+        w = (torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16)
+        b = (torch.randn(n, generator=gen) * 0.01).to(torch.bfloat16) if bias else None
+        if fmt == "int8":
+            q_w, s_w = TP.quantize_weight_int8(w)
+            quant = lambda: TP.quantize_act_int8_vllm(x)  # noqa: E731
+            q_a, s_a = quant()
+            gemm = lambda: TP.int8_linear(q_a, s_a, q_w, s_w)  # noqa: E731
+        else:
+            q_w, s_w = TP.quantize_rows_e4m3(w)
+            quant = lambda: TP.quantize_rows_e4m3(x)  # noqa: E731
+            q_a, s_a = quant()
+            gemm = lambda: TP.fp8_linear(q_a, s_a, q_w, s_w, b)  # noqa: E731
+        t_q, t_g = med(quant), med(gemm)
+        rec = {"M": m, "K": k, "N": n, "rows_timed": rows,
+               "act_quant_GB/s": round((3 * rows * k + 4 * rows) / t_q / 1e9, 3),
+               "gemm_TFLOP/s" if fmt != "int8" else "gemm_TOP/s": round(2.0 * rows * n * k / t_g / 1e12, 4)}
+        t_all = t_q + t_g
+        if lora:
+            la = (torch.randn(128, k, generator=gen) * 0.01).to(torch.bfloat16)
+            lb = (torch.randn(n, 128, generator=gen) * 0.01).to(torch.bfloat16)
+            base = gemm()
+            t_l = med(lambda: TP.lora_update(x, base, la, lb, 1.0))
+            rec["lora_GFLOP/s"] = round(2.0 * rows * 128 * (k + n) / t_l / 1e9, 2)
+            t_all += t_l
+        rec["end_to_end_ms_full_M"] = round(t_all * m / rows * 1e3, 3)
+        out[name] = rec
+    return out
+
+
 # Secondary measurements, in the order they run.
 EXTRAS = {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "f1": bench_f1, "f4": bench_f4, "a6": bench_a6,
           "h3_qkv_lora": bench_h3_lora, "ceilings": bench_ceilings}
@@ -824,6 +892,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(torch, w_cpu, bias_cpu, x_cpu)
+        result["cpu_baseline"]["per_config"] = cpu_baseline_per_config(torch)
     print(json.dumps(result), flush=True)
     return 0
 

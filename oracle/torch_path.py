@@ -15,6 +15,7 @@ every bf16 value.
                              e4m3fn cast (per-token / per-channel FP8)
 * ``quantize_tensor_e4m3``   FL/inference/fused_kernels.py:771-796 (eager)
 * ``quantize_fp8_e4m3_per_head``  FL/inference/fused_kernels.py:823-834 (eager)
+* ``quantize_act_int8_vllm`` vLLM's dynamic per-token int8 (H3/inference/w8a8.py:178)
 * ``int8_linear``            torch._int_mm then s_a * (s_w * float(acc))
 * ``fp8_linear``             dequant-then-matmul F.linear(q_a.float()*s_a,
                              q_w.float()*s_w, bias) -> bf16 (BASELINE CPU plan)
@@ -60,6 +61,16 @@ def quantize_fp8_e4m3_per_head(value: torch.Tensor) -> tuple[torch.Tensor, torch
     scale = torch.clamp(scalar_div(value.float().abs().amax(dim=(1, 3)), FP8_MAX), min=1.0e-12)
     quantized = torch.clamp(value / scale[:, None, :, None], -FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
     return quantized, scale
+
+
+def quantize_act_int8_vllm(value: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """vLLM 0.11.1's published dynamic per-token int8 form (called at
+    H3/inference/w8a8.py:178): s = amax / 127, q = sat8(rint(x * (127 / amax))),
+    a zero row giving zero codes (TEST INFRASTRUCTURE: the CPU baseline's act-quant)."""
+    amax = value.abs().amax(dim=1, keepdim=True).float()
+    inv = torch.where(amax > 0, 127.0 / amax, torch.zeros_like(amax))
+    quantized = torch.clamp(torch.round(value.float() * inv), -128, 127).to(torch.int8)
+    return quantized.contiguous(), (amax / 127.0).contiguous()
 
 
 def int8_linear(q_a: torch.Tensor, s_a: torch.Tensor, q_w: torch.Tensor, s_w: torch.Tensor) -> torch.Tensor:
