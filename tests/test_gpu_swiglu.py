@@ -53,7 +53,9 @@ def _check(ops, oracle, device, x, fmt, rounding, want_out=True, want_codes=True
 
 @pytest.mark.parametrize("fmt,rounding", FMTS)
 @pytest.mark.parametrize("rows,half", [(64, 1024), (37, 5376), (9, 7168), (5, 14336), (3, 16384), (130, 2048),
-                                       (2, 8), (17, 1000)])
+                                       (2, 8), (17, 1000),
+                                       # 1024 rows and more: the table form (s looked up per gate pattern)
+                                       (1024, 1024), (1061, 13824), (1030, 14336)])
 def test_swiglu_matches_oracle(ops, oracle, device, fmt, rounding, rows, half):
     _check(ops, oracle, device, _inputs(rows, half, seed=rows + half), fmt, rounding)
 
@@ -88,17 +90,20 @@ def test_special_values(ops, oracle, device):
     np.testing.assert_array_equal(bits16(out), oracle.swiglu(bits16(x)))
 
 
-def test_every_bf16_gate(ops, oracle, device):
+@pytest.mark.parametrize("rows", [64, 1024])
+def test_every_bf16_gate(ops, oracle, device, rows):
     """silu depends on the gate alone, so the 65536 bf16 gate values (NaNs,
     infinities, subnormals and both zeros included) with up = 1 cover it
     completely: y = bf16(silu(gate)) bit-exact against the oracle, whose exp
     is the IEEE-only restatement while the kernel uses the hardware exp2.
-    NaN gates must give NaN (the payload is not compared)."""
-    gate = np.arange(65536, dtype=np.uint32).astype(np.uint16).reshape(64, 1024)
-    up = np.full((64, 1024), 0x3F80, dtype=np.uint16)  # bf16 1.0
+    NaN gates must give NaN (the payload is not compared).  64 rows run the
+    direct form; 1024 rows the table form, whose device table this covers
+    entry by entry."""
+    gate = np.arange(65536, dtype=np.uint32).astype(np.uint16).reshape(rows, 65536 // rows)
+    up = np.full(gate.shape, 0x3F80, dtype=np.uint16)  # bf16 1.0
     xb = np.concatenate([gate, up], axis=1)
     x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)
-    print("swiglu every bf16 gate (64 x 1024, up = 1)", flush=True)
+    print(f"swiglu every bf16 gate ({rows} rows, up = 1)", flush=True)
     out, _, _ = ops.swiglu_quant(x.to(device), out=True)
     torch.cuda.synchronize()
     got, want = bits16(out), oracle.swiglu(xb)
