@@ -383,7 +383,7 @@ ORC_API void orc_quant_tensor_e4m3_typed(const void* x, int dtype, int eager, in
         for (int64_t i = 0; i < rows; ++i)
             for (int64_t j = 0; j < k; ++j) {
                 float a = fabsf(typed_load(x, dtype, i * ldx + j));
-                if (a > amax) amax = a;
+                if (a > amax || isnan(a)) amax = a;
             }
         s = amax_scale(amax, kE4M3Max);
     }
@@ -548,9 +548,9 @@ static float round_bf16_ref(float f) {
 /* For each row r (t = indices[r]):
  *   [branch] h = bf16(residual + bf16(gate[t] * branch))  -> hidden
  *   v = branch ? h : value
- *   ss: 64 lane sums, lane l adding v[8 (l + 64 i) + e]^2 (product rounded, then
- *       the sum) in ascending (i, e); then 6 butterfly steps s_l += s_(l xor d),
- *       d = 32, 16, ..., 1
+ *   ss: 64 lane sums, lane l adding v[8 (l + 64 i) + e]^2 by one fused
+ *       multiply-add each (s = fma(v, v, s)) in ascending (i, e); then 6
+ *       butterfly steps s_l += s_(l xor d), d = 32, 16, ..., 1
  *   rs = 1 / sqrt(ss / cols + eps)   (each operation an IEEE binary32 operation)
  *   n  = bf16((v * rs) * weight);  y = bf16(bf16(n * bf16(1 + scale[t])) + shift[t])
  * cols must be a multiple of 8.  hidden may be NULL without branch. */
@@ -582,8 +582,7 @@ ORC_API void orc_rms_norm_modulate(const uint16_t* value, int64_t ldv, const uin
             for (int64_t vec = l; vec < nvec; vec += 64)
                 for (int e = 0; e < 8; ++e) {
                     const float x = v[8 * vec + e];
-                    const float sq = x * x;
-                    s = s + sq;
+                    s = fmaf(x, x, s);
                 }
             lane[l] = s;
         }

@@ -186,11 +186,11 @@ __global__ __launch_bounds__(256) void quant_rows_any_kernel(const uint16_t* __r
     const int64_t row = blockIdx.x;
     const uint16_t* xr = x + row * ldx;
     float amax = 0.0f;
-    for (int64_t j = threadIdx.x; j < k; j += 256) amax = fmaxf(amax, fabsf(bf16_lo(xr[j])));
+    for (int64_t j = threadIdx.x; j < k; j += 256) amax = mag_max(amax, fabsf(bf16_lo(xr[j])));
     amax = wave_max(amax);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
     __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    amax = mag_max(mag_max(red[0], red[1]), mag_max(red[2], red[3]));
     RowQuant<FMT, ROUND> rq;
     rq.init(amax);
     for (int64_t j = threadIdx.x; j < k; j += 256) {
@@ -325,18 +325,17 @@ struct TensorQuant {
     // (v_cvt_pk_bf16_f32, round to nearest even), clamped, converted.
     __device__ __forceinline__ uint32_t pack2(uint32_t w) const {
         const uint32_t b = pack_bf16x2(quotient(bf16_lo(w)), quotient(bf16_hi(w)));
-        return cvt_e4m3x2(__builtin_amdgcn_fmed3f(bf16_lo(b), -kE4M3Max, kE4M3Max),
-                          __builtin_amdgcn_fmed3f(bf16_hi(b), -kE4M3Max, kE4M3Max));
+        return cvt_e4m3x2(clamp_e4m3(bf16_lo(b)), clamp_e4m3(bf16_hi(b)));
     }
     __device__ __forceinline__ uint32_t pack4(uint32_t w0, uint32_t w1) const { return pack2(w0) | (pack2(w1) << 16); }
 };
 
-// Maximum of a workgroup's per-wave values (non-negative), on every thread.
+// Maximum of a workgroup's per-wave magnitudes (NaN kept), on every thread.
 __device__ __forceinline__ float block_max4(float v, float* red) {
     v = wave_max(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    return mag_max(mag_max(red[0], red[1]), mag_max(red[2], red[3]));
 }
 
 // Scale of pass 2: the static scale, or the fold of the partial maxima
@@ -354,7 +353,7 @@ __device__ __forceinline__ TensorQuant tensor_scale(const float* __restrict__ pa
             const int i = (int)threadIdx.x + 256 * k;
             p[k] = partial[i < nparts ? i : nparts - 1];
         }
-        const float a = block_max4(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])), red);
+        const float a = block_max4(mag_max(mag_max(p[0], p[1]), mag_max(p[2], p[3])), red);
         tq.s = amax_scale(a, kE4M3Recip);
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = tq.s;
@@ -437,7 +436,7 @@ __global__ __launch_bounds__(256) void tensor_amax_any_kernel(const uint16_t* __
     const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
     float amax = 0.0f;
     for (int64_t r = r0; r < r1; ++r)
-        for (int64_t j = threadIdx.x; j < k; j += 256) amax = fmaxf(amax, fabsf(bf16_lo(x[r * ldx + j])));
+        for (int64_t j = threadIdx.x; j < k; j += 256) amax = mag_max(amax, fabsf(bf16_lo(x[r * ldx + j])));
     const float a = block_max4(amax, red);
     if (threadIdx.x == 0) partial[blockIdx.x] = a;
 }
@@ -482,7 +481,7 @@ __global__ __launch_bounds__(256) void tensor_amax_typed_kernel(const void* __re
     const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
     float amax = 0.0f;
     for (int64_t r = r0; r < r1; ++r)
-        for (int64_t j = threadIdx.x; j < k; j += 256) amax = fmaxf(amax, fabsf(load_in<IN>(x, r * ldx + j)));
+        for (int64_t j = threadIdx.x; j < k; j += 256) amax = mag_max(amax, fabsf(load_in<IN>(x, r * ldx + j)));
     const float a = block_max4(amax, red);
     if (threadIdx.x == 0) partial[blockIdx.x] = a;
 }
@@ -510,7 +509,7 @@ __global__ __launch_bounds__(256) void tensor_quant_typed_kernel(const void* __r
             if (rnd == 2) v = (float)(_Float16)v;
             uint32_t code;
             if (v != v) code = 0x7Fu;
-            else code = cvt_e4m3x2(__builtin_amdgcn_fmed3f(v, -kE4M3Max, kE4M3Max), 0.0f) & 0xFFu;
+            else code = cvt_e4m3x2(clamp_e4m3(v), 0.0f) & 0xFFu;
             q[r * ldq + j] = (uint8_t)code;
         }
     }

@@ -67,11 +67,31 @@ __device__ __forceinline__ float round_to_bf16(float f) {
     return __uint_as_float(f32_to_bf16_bits(f) << 16);
 }
 
-// Wavefront-wide maximum of a non-negative float (64 lanes, butterfly).
+// Maximum of two magnitudes (non-negative floats, a NaN among them positive)
+// that keeps a NaN, as torch's amax does: the bits of a magnitude order like
+// its value, and a positive NaN's bits lie above those of +inf.  (fmaxf
+// returns the other operand when one is a NaN.)
+__device__ __forceinline__ float mag_max(float a, float b) {
+    const uint32_t x = __float_as_uint(a), y = __float_as_uint(b);
+    return __uint_as_float(x > y ? x : y);
+}
+
+// Wavefront-wide maximum of a magnitude (64 lanes, butterfly; NaN kept).
 __device__ __forceinline__ float wave_max(float v) {
+    uint32_t b = __float_as_uint(v);
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)b, off, 64);
+        b = b > o ? b : o;
+    }
+    return __uint_as_float(b);
+}
+
+// torch.clamp(v, -448, 448), which leaves a NaN as it is.  (v_med3_f32 alone
+// would not: with a NaN operand it returns the least of the other two, -448.)
+__device__ __forceinline__ float clamp_e4m3(float v) {
+    const float c = __builtin_amdgcn_fmed3f(v, -kE4M3Max, kE4M3Max);
+    return v == v ? c : v;
 }
 
 // Two binary32 values (already clamped to +-448) -> two e4m3fn codes in the

@@ -99,13 +99,13 @@ struct IoElem {
 };
 
 // One position's quantizer: e4m3(x / s) with the correctly rounded binary32
-// quotient (div_rn, r = RN(1/s)).  No clamp: |x| <= amax and s = RN(amax *
+// quotient (div_rn_signed, r = RN(1/s)).  No clamp: |x| <= amax and s = RN(amax *
 // RN(1/448)) give |x / s| <= 448 (1 + 2^-22), which v_cvt_pk_fp8_f32 rounds
 // to 448 (it saturates everything up to 464; measured on MI355X); a NaN
 // quotient stays NaN, as torch's clamp leaves it.
 struct HeadQuant {
     float s, r;
-    __device__ __forceinline__ float value(float f) const { return copysignf(div_rn(f, s, r), f); }
+    __device__ __forceinline__ float value(float f) const { return div_rn_signed(f, s, r); }
     __device__ __forceinline__ uint32_t pack4(uint32_t w0, uint32_t w1) const {
         return cvt_e4m3x2(value(bf16_lo(w0)), value(bf16_hi(w0))) |
                (cvt_e4m3x2(value(bf16_lo(w1)), value(bf16_hi(w1))) << 16);
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void head_scale_kernel(const float* __restrict
     }
     float a = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) a = fmaxf(a, v[k]);
+    for (int k = 0; k < 16; ++k) a = mag_max(a, v[k]);
     a = wave_max(a);
     if (lane == 0) scale_out[bh] = amax_scale(a, kE4M3Recip);
 }

@@ -14,8 +14,9 @@
 // Every binary32 operation is a single IEEE round-to-nearest operation in the
 // order written (no contraction).  The sum of squares has a fixed order:
 // lane l of the row's wavefront accumulates its elements k = 8 (l + 64 i) + e
-// in ascending (i, e), then a butterfly over the 64 lanes (xor 32, 16, ..., 1)
-// adds the lane partial sums.  rs is the IEEE square root followed by an IEEE
+// in ascending (i, e), each by one fused multiply-add (ss = fma(v, v, ss)),
+// then a butterfly over the 64 lanes (xor 32, 16, ..., 1) adds the lane
+// partial sums.  rs is the IEEE square root followed by an IEEE
 // division.  The reference's Triton kernels use the hardware's approximate
 // rsqrt and an unspecified reduction tree, so their rs can differ in the last
 // bits; these kernels instead fix both so that a CPU restatement reproduces
@@ -44,6 +45,12 @@ namespace {
 // plus the lowest kept bit, truncate), infinities included; NaNs come out as
 // NaNs with possibly different payload bits.
 __device__ __forceinline__ uint32_t rb2(float lo, float hi) { return pack_bf16x2(lo, hi); }
+
+// One binary32 value rounded to bf16 and kept as binary32: the same
+// conversion with +0 as the low half leaves bf16(v) in the high half and
+// zeros below it, which is the binary32 value bf16(v) (one instruction, where
+// packing and unpacking again takes one and a half per value).
+__device__ __forceinline__ float rb1(float v) { return __uint_as_float(pack_bf16x2(0.0f, v)); }
 
 // Single IEEE binary32 operations, each rounded to nearest even (contraction
 // is off in this file, so the compiler keeps them separate).
@@ -166,8 +173,8 @@ __global__ __launch_bounds__(256) void norm_modulate_quant_kernel(NormQuantArgs 
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t w = words_of(v[i], j);
-                ss = fadd(ss, fmul(lo_f(w), lo_f(w)));
-                ss = fadd(ss, fmul(hi_f(w), hi_f(w)));
+                ss = __builtin_fmaf(lo_f(w), lo_f(w), ss);
+                ss = __builtin_fmaf(hi_f(w), hi_f(w), ss);
             }
         }
 #pragma unroll
@@ -205,10 +212,11 @@ __global__ __launch_bounds__(256) void norm_modulate_quant_kernel(NormQuantArgs 
                 for (int j = 0; j < 4; ++j) {
                     const uint32_t xw = words_of(v[i], j), ww = words_of(w[slot][k], j);
                     const uint32_t cw = words_of(sc[slot][k], j), hw = words_of(sh[slot][k], j);
-                    const uint32_t nw = rb2(fmul(fmul(lo_f(xw), rsi), lo_f(ww)), fmul(fmul(hi_f(xw), rsi), hi_f(ww)));
-                    const uint32_t s1 = rb2(fadd(1.0f, lo_f(cw)), fadd(1.0f, hi_f(cw)));
-                    const uint32_t tw = rb2(fmul(lo_f(nw), lo_f(s1)), fmul(hi_f(nw), hi_f(s1)));
-                    y[j] = rb2(fadd(lo_f(tw), lo_f(hw)), fadd(hi_f(tw), hi_f(hw)));
+                    const float n0 = rb1(fmul(fmul(lo_f(xw), rsi), lo_f(ww)));
+                    const float n1 = rb1(fmul(fmul(hi_f(xw), rsi), hi_f(ww)));
+                    const float t0 = rb1(fmul(n0, rb1(fadd(1.0f, lo_f(cw)))));
+                    const float t1 = rb1(fmul(n1, rb1(fadd(1.0f, hi_f(cw)))));
+                    y[j] = rb2(fadd(t0, lo_f(hw)), fadd(t1, hi_f(hw)));
                     m = pk_abs_max(m, y[j]);
                 }
                 v[i] = make_uint4(y[0], y[1], y[2], y[3]);

@@ -38,6 +38,18 @@ H3Q_HD float div_rn(float x, float s, float r) {
     return fmaf(e, r, q0);
 }
 
+// The same quotient with the sign of a zero dividend kept, so that no
+// copysign has to follow: the residual is formed with the opposite sign,
+//   q0 = RN(x * r);  e = q0 * s - x (exact, one fma);  q1 = RN(q0 - e * r),
+// the value of div_rn for every nonzero x, and +-0 for x = +-0 (q0 = +-0,
+// e = +0, q1 = -0 * r + q0 = q0) where div_rn gives +0.  The test suite
+// checks it against IEEE division over the same set, signs included.
+H3Q_HD float div_rn_signed(float x, float s, float r) {
+    const float q0 = x * r;
+    const float e = fmaf(q0, s, -x);
+    return fmaf(-e, r, q0);
+}
+
 // The same quotient for any binary32 divisor (a static, calibrated scale or
 // one rounded to bf16): where the three operations leave a non-finite value
 // (the quotient or the reciprocal overflows, s is 0, inf or NaN, x is inf or

@@ -28,10 +28,18 @@ __device__ __forceinline__ int sat_int(float v, int lo) {
     return i < lo ? lo : (i > 127 ? 127 : i);
 }
 
-// One row element -> code, for each quantizer form.
+// One row element -> code, for each quantizer form.  The scale is always the
+// row's own (from the maximum of |x| over the row), which the e4m3 form relies
+// on: |x| <= amax and s = max(RN(amax * RN(1/448)), 1e-12) give
+// |x / s| <= 448 (1 + 2^-22), which v_cvt_pk_fp8_f32 rounds to 448 (it
+// saturates everything up to 464; measured on MI355X), so the reference's
+// clamp to +-448 changes no code and is not applied; a NaN quotient stays NaN,
+// as torch's clamp leaves it.
 template <int FMT, int ROUND>
 struct RowQuant {
-    float s, r;  // DIV: scale and RN(1/scale); RCP: scale and 127/amax
+    // DIV: scale, RN(1/scale) and the divisor of the residual correction;
+    // RCP: scale and 127/amax.
+    float s, r, dv;
     __device__ __forceinline__ void init(float amax) {
         if (ROUND == kRoundRcpMul) {
             s = amax / kInt8Max;
@@ -39,24 +47,24 @@ struct RowQuant {
         } else {
             s = amax_scale(amax, FMT == kFmtE4M3 ? kE4M3Recip : kInt8Recip);
             r = 1.0f / s;
+            // A row holding an infinity has s = inf and r = 0, where the
+            // correction's q0 * s - x would be 0 * inf = NaN although x / s is
+            // +-0.  With dv = 0 the correction adds x * 0 to q0 = x * 0: +-0 for
+            // a finite x and NaN (inf * 0) for an infinite one, the IEEE
+            // quotients.  For a finite s, dv = s.
+            dv = s <= 3.402823466e38f ? s : 0.0f;
         }
     }
     __device__ __forceinline__ float value(float f) const {
         if (ROUND == kRoundRcpMul) return __builtin_rintf(f * r);
-        float q = copysignf(div_rn(f, s, r), f);
+        const float q = div_rn_signed(f, dv, r);
         return FMT == kFmtE4M3 ? q : __builtin_rintf(q);
     }
     // 4 bf16 (two packed words) -> 4 code bytes.
     __device__ __forceinline__ uint32_t pack4(uint32_t w0, uint32_t w1) const {
-        float a = value(bf16_lo(w0)), b = value(bf16_hi(w0));
-        float c = value(bf16_lo(w1)), d = value(bf16_hi(w1));
-        if (FMT == kFmtE4M3) {
-            a = __builtin_amdgcn_fmed3f(a, -kE4M3Max, kE4M3Max);
-            b = __builtin_amdgcn_fmed3f(b, -kE4M3Max, kE4M3Max);
-            c = __builtin_amdgcn_fmed3f(c, -kE4M3Max, kE4M3Max);
-            d = __builtin_amdgcn_fmed3f(d, -kE4M3Max, kE4M3Max);
-            return cvt_e4m3x2(a, b) | (cvt_e4m3x2(c, d) << 16);
-        }
+        const float a = value(bf16_lo(w0)), b = value(bf16_hi(w0));
+        const float c = value(bf16_lo(w1)), d = value(bf16_hi(w1));
+        if (FMT == kFmtE4M3) return cvt_e4m3x2(a, b) | (cvt_e4m3x2(c, d) << 16);
         // Saturating convert: v_cvt_i32_f32 maps NaN to 0 and +-inf to the
         // int32 limits, then an integer clamp (NaN -> 0, inf -> 127 / lo as
         // in a saturating int8 convert).

@@ -3,9 +3,11 @@
 Every divisor a quantizer forms is max(amax * RN(1/L), 1e-12) for a bf16
 amax (L = 127 or 448; amax_scale) and every dividend is a bf16 x with
 |x| <= amax.  Over all
-~1.07e9 such pairs per L, div_rn(x, s, RN(1/s)) (three fused ops) must equal
-IEEE x / s bit for bit, except where |x / s| < 2^-70 (the residual underflows),
-where both quotients produce the same code 0.  The header is compiled with
+~1.07e9 such pairs per L, div_rn(x, s, RN(1/s)) (three fused ops, its sign
+restored by copysign) and div_rn_signed (the form the per-row quantizers use,
+no copysign) must equal IEEE x / s bit for bit, except where
+|x / s| < 2^-70 (the residual underflows), where both quotients have x's sign
+and produce the same code +-0.  The header is compiled with
 g++ exactly as the device includes it."""
 
 from __future__ import annotations
@@ -27,8 +29,8 @@ int main(){
   for (int lim=0; lim<2; ++lim){
     const float L = lim ? h3q::kE4M3Max : h3q::kInt8Max;
     const float R = lim ? h3q::kE4M3Recip : h3q::kInt8Recip;
-    long long bad_big = 0, bad_small = 0, total = 0;
-    #pragma omp parallel for schedule(dynamic,64) reduction(+:bad_big,bad_small,total)
+    long long bad_big = 0, bad_small = 0, bad_sign = 0, total = 0;
+    #pragma omp parallel for schedule(dynamic,64) reduction(+:bad_big,bad_small,bad_sign,total)
     for (uint32_t ah = 0; ah < 0x7F80; ++ah) {
       const float amax = bf((uint16_t)ah);
       const float s = h3q::amax_scale(amax, R);
@@ -38,14 +40,18 @@ int main(){
           const float x = bf((uint16_t)(xh | (sg << 15)));
           const float a = x / s;
           const float b = copysignf(h3q::div_rn(x, s, r), x);
-          uint32_t ab, bb; memcpy(&ab, &a, 4); memcpy(&bb, &b, 4);
+          const float c = h3q::div_rn_signed(x, s, r);
+          uint32_t ab, bb, cb; memcpy(&ab, &a, 4); memcpy(&bb, &b, 4); memcpy(&cb, &c, 4);
           ++total;
           if (ab != bb) { if (fabsf(a) >= 0x1p-70f || fabsf(b) >= 0x1p-70f) ++bad_big; else ++bad_small; }
+          if (ab != cb) { if (fabsf(a) >= 0x1p-70f || fabsf(c) >= 0x1p-70f) ++bad_big; else ++bad_small; }
+          if ((ab ^ cb) & 0x80000000u) ++bad_sign;
         }
       }
     }
-    printf("L=%g pairs=%lld mismatches_above_2^-70=%lld tiny=%lld\n", L, total, bad_big, bad_small);
-    if (bad_big) rc = 1;
+    printf("L=%g pairs=%lld mismatches_above_2^-70=%lld tiny=%lld sign=%lld\n", L, total, bad_big, bad_small,
+           bad_sign);
+    if (bad_big || bad_sign) rc = 1;
   }
   return rc;
 }

@@ -63,6 +63,38 @@ def test_typed_tensor_quant_is_the_reference_expression_on_the_device(ops, devic
     np.testing.assert_array_equal(bits8(q), bits8(ref))
 
 
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+@pytest.mark.parametrize("static", [False, True])
+def test_typed_tensor_quant_infinities_and_nans_on_the_device(ops, oracle, device, dtype, static):
+    """With infinities and a NaN in the tensor: the reference's eager
+    expression evaluated by torch on this GPU, the kernel and the oracle
+    agree (a dynamic scale is NaN, every code NaN; under a static scale the
+    infinities saturate to +-448 and the NaN stays NaN).  NaN codes are
+    compared as NaN."""
+    x = _inputs(300, 512, 9, dtype)
+    x[7, 3] = float("inf")
+    x[100, 500] = float("-inf")
+    x[250, 0] = float("nan")
+    xd = x.to(device)
+    st = 0.0371 if static else None
+    if static:
+        scale = torch.tensor(st, dtype=torch.float32, device=device)
+        q, s = ops.quant_tensor_e4m3(xd, scale, eager=True)
+    else:
+        scale = torch.clamp(xd.detach().abs().amax().to(torch.float32) / 448.0, min=1.0e-12)
+        q, s = ops.quant_tensor_e4m3(xd, eager=True)
+    ref = torch.clamp(xd / scale, -448.0, 448.0).to(torch.float8_e4m3fn)
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_tensor_e4m3_typed(_bits(x), dtype, True, st)
+    for sv in (scale.item(), rs):
+        assert (np.isnan(s.item()) and np.isnan(sv)) or s.item() == sv
+    got = bits8(q)
+    for want in (bits8(ref), rq):
+        nan_q = (want & 0x7F) == 0x7F
+        np.testing.assert_array_equal((got & 0x7F) == 0x7F, nan_q)
+        np.testing.assert_array_equal(np.where(nan_q, 0, got), np.where(nan_q, 0, want))
+
+
 def test_typed_tensor_quant_all_zero_fp16(ops, device):
     """fp16(1e-12) == 0: the eager quotient is 0 / 0 and every code is NaN,
     as in the reference.  The NaN's sign is the device's: the reference's

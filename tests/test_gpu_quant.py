@@ -99,6 +99,88 @@ def test_rows_extreme_magnitudes(ops, oracle, device, fmt, rounding):
     _check_rows(ops, oracle, x.to(torch.bfloat16), device, fmt, rounding)
 
 
+def _special_rows(k: int) -> torch.Tensor:
+    """Rows holding infinities and NaNs among finite values (and one plain
+    row): an infinite amax makes the scale infinite, a NaN amax makes it NaN."""
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(6, k, generator=gen)
+    x[0, 17] = float("inf")
+    x[1, 3] = float("-inf")
+    x[1, 5] = float("inf")
+    x[2, 40] = float("nan")
+    x[3, 0] = float("nan")
+    x[3, k - 1] = float("inf")
+    x[5, :] = float("inf")
+    return x.to(torch.bfloat16)
+
+
+def _check_special(q, s, rq, rs, fmt):
+    """Codes equal the oracle's, NaN codes compared as NaN (their sign bit is
+    not fixed by the reference: the sign of x / s for a NaN s is unspecified);
+    scales equal bit for bit, NaN scales as NaN."""
+    nan_s = np.isnan(rs)
+    np.testing.assert_array_equal(np.isnan(s), nan_s)
+    np.testing.assert_array_equal(s[~nan_s], rs[~nan_s])
+    if fmt == "e4m3":
+        want = rq.view(np.uint8)
+        nan_q = (want & 0x7F) == 0x7F
+        np.testing.assert_array_equal((q & 0x7F) == 0x7F, nan_q)
+        np.testing.assert_array_equal(np.where(nan_q, 0, q), np.where(nan_q, 0, want))
+    else:
+        np.testing.assert_array_equal(q, rq.view(np.uint8))
+
+
+@pytest.mark.parametrize("fmt,rounding", [("e4m3", "div"), ("int8", "div")])
+@pytest.mark.parametrize("k", [640, 5120, 1000])
+def test_rows_with_infinities_and_nans(ops, oracle, device, fmt, rounding, k):
+    """x / s with s = inf is +-0 for finite x and NaN for x = +-inf (IEEE
+    division, the reference's torch expression); a NaN in the row gives a NaN
+    scale and NaN quotients.  Row-major (vector and general kernels) and
+    tiled codes."""
+    from _util import from_tiled
+
+    print(f"rows with inf / nan {fmt} k={k}", flush=True)
+    x = _special_rows(k)
+    xb = bits16(x)
+    rq, rs = oracle.quant_rows(xb, fmt, rounding)
+    q, s = _run_rows(ops, x.to(device), fmt, rounding)
+    _check_special(q, s, rq, rs, fmt)
+    if k % 128 == 0:
+        f = ops.FMT_E4M3FN if fmt == "e4m3" else ops.FMT_INT8
+        qt, st = ops.quant_rows_tiled(x.to(device), f, ops.ROUND_DIV)
+        torch.cuda.synchronize()
+        _check_special(from_tiled(bits8(qt), qt.shape[0], k)[:x.shape[0]], st.cpu().numpy().ravel(), rq, rs, fmt)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "int8"])
+def test_rows_with_infinities_and_nans_match_the_reference_on_the_gpu(ops, device, fmt):
+    """The same rows through the reference's own torch expressions evaluated
+    on this GPU (H3/inference/w8a8.py:57-63 and its e4m3 counterpart): equal
+    codes and scales, NaN codes compared as NaN; for int8, positions whose
+    quotient is NaN are left out (torch's float -> int8 cast of a NaN is not
+    defined)."""
+    from oracle import torch_path as TP
+
+    xd = _special_rows(1024).to(device)
+    if fmt == "e4m3":
+        tq, ts = TP.quantize_rows_e4m3(xd)
+        q, s = ops.quant_rows(xd, ops.FMT_E4M3FN, ops.ROUND_DIV)
+    else:
+        tq, ts = TP.quantize_weight_int8(xd)
+        q, s = ops.quant_rows(xd, ops.FMT_INT8, ops.ROUND_DIV)
+    torch.cuda.synchronize()
+    got_s, want_s = s.cpu().numpy().ravel(), ts.cpu().numpy().ravel()
+    np.testing.assert_array_equal(np.isnan(got_s), np.isnan(want_s))
+    np.testing.assert_array_equal(got_s[~np.isnan(want_s)], want_s[~np.isnan(want_s)])
+    got, want = bits8(q), bits8(tq)
+    if fmt == "e4m3":
+        skip = (want & 0x7F) == 0x7F
+        np.testing.assert_array_equal((got & 0x7F) == 0x7F, skip)
+    else:
+        skip = torch.isnan(xd.float() / ts).cpu().numpy()
+    np.testing.assert_array_equal(np.where(skip, 0, got), np.where(skip, 0, want))
+
+
 # Shapes include the c2 activations (8192 x 5120) and row counts past the
 # 1024-workgroup grid of the two passes (several rows per wave).
 @pytest.mark.parametrize("static", [False, True])
@@ -129,6 +211,36 @@ def test_tensor_e4m3_bf16_divisor_matches_oracle(ops, oracle, device, static, m,
     rq, rs = oracle.quant_tensor_e4m3(bits16(x), st, bf16_divisor=True)
     assert np.float32(s.item()) == rs
     np.testing.assert_array_equal(bits8(q), rq)
+
+
+@pytest.mark.parametrize("case", ["inf", "nan", "static"])
+@pytest.mark.parametrize("bf16_divisor", [False, True])
+def test_tensor_e4m3_infinities_and_nans(ops, oracle, device, case, bf16_divisor):
+    """An infinity in the tensor makes the dynamic scale infinite (finite
+    elements -> +-0, infinite ones -> NaN); a NaN makes it NaN (every code
+    NaN); under a static scale an infinity saturates to +-448 and a NaN stays
+    NaN (torch.clamp keeps it; v_med3 alone would give -448).  NaN codes are
+    compared as NaN (their sign is not fixed by the reference)."""
+    x = activations(1000, 5120, seed=21)
+    if case in ("inf", "static"):
+        x[3, 17] = float("inf")
+        x[999, 5119] = float("-inf")
+    if case in ("nan", "static"):
+        x[500, 2] = float("nan")
+    xb = bits16(x)
+    st = 0.0371 if case == "static" else None
+    sg = torch.tensor(st, dtype=torch.float32, device=device) if st else None
+    q, s = ops.quant_tensor_e4m3(x.to(device), sg, bf16_divisor=bf16_divisor)
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_tensor_e4m3(xb, st, bf16_divisor=bf16_divisor)
+    s = np.float32(s.item())
+    assert (np.isnan(s) and np.isnan(rs)) or s == rs
+    got, want = bits8(q), rq.view(np.uint8)
+    nan_q = (want & 0x7F) == 0x7F
+    np.testing.assert_array_equal((got & 0x7F) == 0x7F, nan_q)
+    np.testing.assert_array_equal(np.where(nan_q, 0, got), np.where(nan_q, 0, want))
+    if case == "static":
+        assert got[3, 17] == 0x7E and got[999, 5119] == 0xFE
 
 
 def test_tensor_e4m3_3d_input(ops, oracle, device):
