@@ -267,6 +267,7 @@ hipError_t launch_nq_fmt(const NormQuantArgs& a, bool resid, hipStream_t st) {
     if (nvec <= 128) return launch_nq_nv<FMT, ROUND, 2>(a, resid, st);
     if (nvec <= 256) return launch_nq_nv<FMT, ROUND, 4>(a, resid, st);
     if (nvec <= 512) return launch_nq_nv<FMT, ROUND, 8>(a, resid, st);
+    if (nvec <= 640) return launch_nq_nv<FMT, ROUND, 10>(a, resid, st);  // K = 5120 exactly
     if (nvec <= 704) return launch_nq_nv<FMT, ROUND, 11>(a, resid, st);
     return launch_nq_nv<FMT, ROUND, 16>(a, resid, st);
 }

@@ -289,6 +289,7 @@ hipError_t launch_sq_fmt(const SwigluQuantArgs& a, hipStream_t st) {
     if (nvec <= 256) return launch_sq_nv<FMT, ROUND, 4>(a, st);
     if (nvec <= 512) return launch_sq_nv<FMT, ROUND, 8>(a, st);
     if (nvec <= 1024) return launch_sq_nv<FMT, ROUND, 16>(a, st);
+    if (nvec <= 1728) return launch_sq_nv<FMT, ROUND, 27>(a, st);  // F = 13824 exactly
     if (nvec <= 1792) return launch_sq_nv<FMT, ROUND, 28>(a, st);
     return launch_sq_nv<FMT, ROUND, 32>(a, st);
 }
