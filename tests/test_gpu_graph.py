@@ -53,3 +53,39 @@ def test_graph_replays_match_eager(ops, device):
         assert torch.equal(q_a.view(torch.uint8), rq.view(torch.uint8))
         assert torch.equal(s_a.reshape(-1), rs.reshape(-1))
         assert (bits16(out) == bits16(ref)).all()
+
+
+@pytest.mark.parametrize("rows,half", [(1024, 1024), (1030, 13824)])
+def test_swiglu_table_form_in_a_graph(ops, device, rows, half):
+    """The SwiGLU + e4m3 producer at table-form sizes (>= 1024 rows): an eager
+    call builds the device's silu table, a captured call then replays with new
+    inputs and gives the eager codes, scales and bf16 rows bit for bit."""
+    gen = torch.Generator().manual_seed(rows + half)
+    x = (torch.randn(rows, 2 * half, generator=gen) * 3.0).to(torch.bfloat16).to(device)
+    out = torch.empty(rows, half, device=device, dtype=torch.bfloat16)
+    codes = torch.empty(rows, half, device=device, dtype=torch.float8_e4m3fn)
+    scales = torch.empty(rows, 1, device=device, dtype=torch.float32)
+
+    def step():
+        ops.swiglu_quant(x, fmt=ops.FMT_E4M3FN, out=out, codes=codes, scales=scales)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    for replay in range(3):
+        print(f"swiglu graph replay {replay} ({rows} x {half})", flush=True)
+        x.copy_((torch.randn(rows, 2 * half, generator=gen) * 3.0).to(torch.bfloat16).to(device))
+        r_out, r_codes, r_scales = ops.swiglu_quant(x, fmt=ops.FMT_E4M3FN, out=True)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert (bits16(out) == bits16(r_out)).all()
+        assert torch.equal(codes.view(torch.uint8), r_codes.view(torch.uint8))
+        assert torch.equal(scales.reshape(-1), r_scales.reshape(-1))
