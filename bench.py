@@ -102,6 +102,29 @@ def time_in_step(torch, quant, gemm, iters: int):
     return (sum(e[0].elapsed_time(e[1]) for e in evs) / iters, sum(e[1].elapsed_time(e[2]) for e in evs) / iters)
 
 
+def settle_clock(torch, replay, block: int = 8, tol: float = 0.01, cap: int = 1024) -> dict:
+    """Untimed replays of the captured step, in blocks, until the GPU's clock
+    has settled: the sync gaps before the timed region (the eager pass, the
+    capture) let it drop, and it takes ~10-20 ms of load to come back, so the
+    first timed steps would otherwise run slower than every later one.  Stops
+    when a block's median device time is within ``tol`` of the previous
+    block's (or after ``cap`` replays); returns the count and the medians."""
+    medians, done = [], 0
+    while done < cap:
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(block + 1)]
+        ev[0].record()
+        for i in range(block):
+            replay(done + i)
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        done += block
+        t = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(block))[block // 2] * 1e3
+        medians.append(round(t, 1))
+        if len(medians) > 1 and t >= medians[-2] * (1.0 - tol):
+            break
+    return {"replays": done, "block_median_us": medians}
+
+
 def _c3_lora_module(torch, qw, sw, la, lb):
     """A column-parallel FP8 W8A8 base (tiled e4m3 weight + per-channel scales,
     no bias) under the reference's LoRA wrapper, swapped by
@@ -761,6 +784,7 @@ def main() -> int:
     for i in range(args.warmup):
         graphs[i % rotations].replay()
     torch.cuda.synchronize()
+    settle = settle_clock(torch, lambda i: graphs[i % rotations].replay())
 
     # Timed region: exactly K steps (graph replays) between two synchronisations.
     # An event after each replay, on the replay stream, gives every step's
@@ -824,6 +848,8 @@ def main() -> int:
             "launch": "one HIP graph per step (act-quant + GEMM), replayed",
         },
         "eager_ms_per_step": round(eager_elapsed / args.steps * 1e3, 4),
+        # untimed replays after the W warm-up steps, until the step time stopped falling
+        "settle": settle,
         # device time of each timed step (events between the replays, in order):
         # a falling sequence is the clock still settling, a flat one a fixed cost
         "step_replay_us": {
