@@ -247,9 +247,16 @@ hipError_t silu_table_for(hipStream_t st, const uint16_t** out, int* cus) {
         if (e != hipSuccess) return e;
         e = hipDeviceGetAttribute(&cu_count[dev], hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
+        // The wait below is legal even while another stream of this thread
+        // is being captured in global mode: relaxed mode for the fill only.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        e = hipThreadExchangeStreamCaptureMode(&mode);
+        if (e != hipSuccess) return e;
         hipLaunchKernelGGL(silu_table_kernel, dim3(65536 / 512), dim3(256), 0, st, (uint16_t*)ptr);
         e = hipGetLastError();
         if (e == hipSuccess) e = hipStreamSynchronize(st);
+        const hipError_t restore = hipThreadExchangeStreamCaptureMode(&mode);
+        if (e == hipSuccess) e = restore;
         if (e != hipSuccess) return e;
         tables[dev] = (const uint16_t*)ptr;
     }

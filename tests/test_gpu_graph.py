@@ -89,3 +89,53 @@ def test_swiglu_table_form_in_a_graph(ops, device, rows, half):
         assert (bits16(out) == bits16(r_out)).all()
         assert torch.equal(codes.view(torch.uint8), r_codes.view(torch.uint8))
         assert torch.equal(scales.reshape(-1), r_scales.reshape(-1))
+
+
+_FIRST_CALL_DURING_CAPTURE = r'''
+import sys
+sys.path.insert(0, sys.argv[1])
+import torch
+import __graft_entry__
+__graft_entry__.load_package()
+from taomate_h3_amd import ops
+dev = torch.device("cuda:0")
+gen = torch.Generator().manual_seed(5)
+x = (torch.randn(1024, 2048, generator=gen) * 3.0).to(torch.bfloat16).to(dev)
+a = torch.zeros(4, device=dev)
+out = torch.empty(1024, 1024, device=dev, dtype=torch.bfloat16)
+codes = torch.empty(1024, 1024, device=dev, dtype=torch.float8_e4m3fn)
+scales = torch.empty(1024, 1, device=dev, dtype=torch.float32)
+plain = torch.cuda.Stream()
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):            # torch's default: global capture mode
+    a.add_(1.0)                      # captured on torch's capture stream
+    with torch.cuda.stream(plain):   # this process's first table-form call, on a stream not being captured
+        ops.swiglu_quant(x, fmt=ops.FMT_E4M3FN, out=out, codes=codes, scales=scales)
+torch.cuda.synchronize()
+g.replay()
+torch.cuda.synchronize()
+ref_out, ref_codes, ref_scales = ops.swiglu_quant(x, fmt=ops.FMT_E4M3FN, out=True)
+torch.cuda.synchronize()
+assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
+assert torch.equal(codes.view(torch.uint8), ref_codes.view(torch.uint8))
+assert torch.equal(scales, ref_scales)
+assert a.tolist() == [1.0] * 4
+print("ok")
+'''
+
+
+def test_swiglu_table_first_built_while_another_stream_captures(device):
+    """The silu table is built on a process's first table-form call, with a
+    wait for it; that call may come on a plain stream while another stream
+    of the thread is being captured in global mode (where a plain wait is
+    refused), and must then build the table without disturbing the capture.
+    A fresh process, so that this is its first call."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parents[1])
+    res = subprocess.run([sys.executable, "-c", _FIRST_CALL_DURING_CAPTURE, root], capture_output=True, text=True,
+                         timeout=240)
+    assert res.returncode == 0 and res.stdout.strip().endswith("ok"), res.stdout + res.stderr
