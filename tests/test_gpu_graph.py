@@ -125,6 +125,52 @@ print("ok")
 '''
 
 
+_FIRST_CALL_CAPTURED = r'''
+import sys
+sys.path.insert(0, sys.argv[1])
+import torch
+import __graft_entry__
+__graft_entry__.load_package()
+from taomate_h3_amd import ops
+dev = torch.device("cuda:0")
+gen = torch.Generator().manual_seed(6)
+x = (torch.randn(1024, 2048, generator=gen) * 3.0).to(torch.bfloat16).to(dev)
+out = torch.empty(1024, 1024, device=dev, dtype=torch.bfloat16)
+codes = torch.empty(1024, 1024, device=dev, dtype=torch.float8_e4m3fn)
+scales = torch.empty(1024, 1, device=dev, dtype=torch.float32)
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):            # this process's first call, captured: the direct form
+    ops.swiglu_quant(x, fmt=ops.FMT_E4M3FN, out=out, codes=codes, scales=scales)
+torch.cuda.synchronize()
+for i in range(3):
+    x.copy_((torch.randn(1024, 2048, generator=gen) * 3.0).to(torch.bfloat16).to(dev))
+    ref_out, ref_codes, ref_scales = ops.swiglu_quant(x, fmt=ops.FMT_E4M3FN, out=True)  # eager: the table form
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
+    assert torch.equal(codes.view(torch.uint8), ref_codes.view(torch.uint8))
+    assert torch.equal(scales, ref_scales)
+print("ok")
+'''
+
+
+def test_swiglu_first_call_captured_runs_the_direct_form(device):
+    """A process whose first table-form-sized call is captured into a graph
+    (its stream capturing, no table yet) captures the direct form; its
+    replays equal the eager calls that follow, which build the table and take
+    the table form: the two forms give the same bits.  A fresh process."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parents[1])
+    res = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED, root], capture_output=True, text=True,
+                         timeout=240)
+    assert res.returncode == 0 and res.stdout.strip().endswith("ok"), res.stdout + res.stderr
+
+
 def test_swiglu_table_first_built_while_another_stream_captures(device):
     """The silu table is built on a process's first table-form call, with a
     wait for it; that call may come on a plain stream while another stream
