@@ -104,8 +104,16 @@ struct IoElem {
 // to 448 (it saturates everything up to 464; measured on MI355X); a NaN
 // quotient stays NaN, as torch's clamp leaves it.
 struct HeadQuant {
-    float s, r;
-    __device__ __forceinline__ float value(float f) const { return div_rn_signed(f, s, r); }
+    float r, dv;  // RN(1/s) and the divisor of the residual correction
+    // A head holding an infinity has s = inf and r = 0, where the residual
+    // q0 * s - x would be 0 * inf = NaN although x / s is +-0; dividing by 0
+    // there leaves q0 = x * 0: +-0 for a finite x, NaN for an infinite one,
+    // the IEEE quotients.  For a finite s, dv = s.
+    __device__ __forceinline__ void set(float s) {
+        r = 1.0f / s;
+        dv = s <= 3.402823466e38f ? s : 0.0f;
+    }
+    __device__ __forceinline__ float value(float f) const { return div_rn_signed(f, dv, r); }
     __device__ __forceinline__ uint32_t pack4(uint32_t w0, uint32_t w1) const {
         return cvt_e4m3x2(value(bf16_lo(w0)), value(bf16_hi(w0))) |
                (cvt_e4m3x2(value(bf16_lo(w1)), value(bf16_hi(w1))) << 16);
@@ -210,8 +218,7 @@ __global__ __launch_bounds__(256) void head_quant_kernel(const uint16_t* __restr
     for (int i = 0; i < NS; ++i) {
         const int pos = c * 64 * NS + lane + 64 * i;
         off[i] = (pos < npos ? pos : npos - 1) * VEC;
-        rq[i].s = sb[off[i] / D];
-        rq[i].r = 1.0f / rq[i].s;
+        rq[i].set(sb[off[i] / D]);
     }
     for (int64_t row = r0 + wave; row < r1; row += 4) {
         const uint16_t* xr = xb + row * row_len;

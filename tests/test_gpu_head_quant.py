@@ -170,3 +170,35 @@ def test_reference_expressions_on_the_gpu_match_the_oracle(oracle, device):
     rq, rs = oracle.quant_per_head_e4m3(bits16(h))
     np.testing.assert_array_equal(bits8(q), rq)
     np.testing.assert_array_equal(s.cpu().numpy(), rs)
+
+
+@pytest.mark.parametrize("shape", [(1, 300, 40, 128), (2, 33, 3, 20)])
+def test_heads_with_infinities_and_nans(ops, oracle, device, shape):
+    """A head holding an infinity gets an infinite scale (its finite elements
+    -> +-0, the infinite ones -> NaN), a head holding a NaN a NaN scale (every
+    code NaN); the other heads are untouched.  Against the oracle and against
+    the reference's eager expression evaluated by torch on this GPU
+    (FL/inference/fused_kernels.py:826-834); NaN codes are compared as NaN."""
+    from oracle import torch_path as TP
+
+    b, s, h, d = shape
+    x = _head_inputs(b, s, h, d, seed=b * s + h)
+    x[0, 5, 1, 2] = float("inf")
+    x[b - 1, s - 1, 1, d - 1] = float("-inf")
+    x[0, 7, 2, 0] = float("nan")
+    print(f"per_head inf/nan shape={shape}", flush=True)
+    xd = x.to(device)
+    codes, scales = ops.quant_per_head_e4m3(xd)
+    tq, ts = TP.quantize_fp8_e4m3_per_head(xd)
+    torch.cuda.synchronize()
+    rq, rs = oracle.quant_per_head_e4m3(bits16(x))
+    got_s = scales.cpu().numpy()
+    for want_s in (ts.cpu().numpy(), rs):
+        np.testing.assert_array_equal(np.isnan(got_s), np.isnan(want_s))
+        np.testing.assert_array_equal(got_s[~np.isnan(want_s)], want_s[~np.isnan(want_s)])
+    assert np.isinf(got_s[0, 1]) and np.isnan(got_s[0, 2])
+    got = bits8(codes)
+    for want in (bits8(tq), rq.view(np.uint8)):
+        nan_q = (want & 0x7F) == 0x7F
+        np.testing.assert_array_equal((got & 0x7F) == 0x7F, nan_q)
+        np.testing.assert_array_equal(np.where(nan_q, 0, got), np.where(nan_q, 0, want))
