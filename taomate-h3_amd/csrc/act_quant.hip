@@ -328,6 +328,37 @@ struct TensorQuant {
         return cvt_e4m3x2(clamp_e4m3(bf16_lo(b)), clamp_e4m3(bf16_hi(b)));
     }
     __device__ __forceinline__ uint32_t pack4(uint32_t w0, uint32_t w1) const { return pack2(w0) | (pack2(w1) << 16); }
+    // The codes of one 16-byte vector (8 bf16), as pack4 twice, with one test
+    // per vector in place of a branch per element: the quotients by the three
+    // operations of div_rn_any (the quotient of a zero kept as q0 = x * r, so
+    // its sign follows a negative static scale as IEEE division does), and if
+    // any of them is not finite (an infinity or NaN in x; a zero, infinite or
+    // NaN scale; an overflowing quotient or reciprocal) the vector is redone
+    // by pack4, whose quotients fall back to IEEE division and whose clamp
+    // keeps a NaN.  A finite quotient needs neither, so the common path clamps
+    // with v_med3 alone.
+    __device__ __forceinline__ uint2 pack8(const uint4& v) const {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        float q[8];
+        bool bad = false;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float f = (j & 1) ? bf16_hi(w[j >> 1]) : bf16_lo(w[j >> 1]);
+            const float q0 = f * r;
+            const float q1 = fmaf(fmaf(-q0, s, f), r, q0);
+            bad |= !__builtin_isfinite(q1);
+            q[j] = f == 0.0f ? q0 : q1;
+        }
+        if (bad) return make_uint2(pack4(v.x, v.y), pack4(v.z, v.w));
+        uint32_t c[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t b = pack_bf16x2(q[2 * j], q[2 * j + 1]);
+            c[j] = cvt_e4m3x2(__builtin_amdgcn_fmed3f(bf16_lo(b), -kE4M3Max, kE4M3Max),
+                              __builtin_amdgcn_fmed3f(bf16_hi(b), -kE4M3Max, kE4M3Max));
+        }
+        return make_uint2(c[0] | (c[1] << 16), c[2] | (c[3] << 16));
+    }
 };
 
 // Maximum of a workgroup's per-wave magnitudes (NaN kept), on every thread.
@@ -417,12 +448,7 @@ __global__ __launch_bounds__(256) void tensor_quant_vec_kernel(const uint16_t* _
         for (int i = 0; i < NV; ++i) v[i] = *reinterpret_cast<const uint4*>(xr + off[i]);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            if (i * 64 + lane < nvec) {
-                uint2 o;
-                o.x = tq.pack4(v[i].x, v[i].y);
-                o.y = tq.pack4(v[i].z, v[i].w);
-                *reinterpret_cast<uint2*>(qr + off[i]) = o;
-            }
+            if (i * 64 + lane < nvec) *reinterpret_cast<uint2*>(qr + off[i]) = tq.pack8(v[i]);
         }
     }
 }
