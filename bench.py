@@ -1,4 +1,4 @@
-"""Benchmark of the FP8 W8A8 DiT linear on one MI355X (BASELINE configs[1]).
+"""Benchmark of the FP8 W8A8 DiT linear on one MI355X (BASELINE.json configs[1]).
 
 One step is one pass of the quantized-linear hot path over one batch of the
 c2 workload (DiT QKV projection at a 480p streaming chunk):
@@ -25,7 +25,7 @@ profiles/gemm_fp8_c2_traffic.json (rocprofv3 FETCH_SIZE / WRITE_SIZE of this
 same command, scaled by a copy of known size) when it belongs to the GEMM
 kernel measured here.
 
-The other BASELINE configurations are timed as secondary objects (not the
+The other BASELINE.json configurations are timed as secondary objects (not the
 headline): ``c3`` FFN up / down at 768p with the rank-128 LoRA epilogue, ``c4``
 skinny M in {16, 64, 128} (weight-streaming, HBM roofline; launches replayed
 from a HIP graph, weights rotated past the Infinity Cache) and ``c5`` the int8
@@ -162,7 +162,7 @@ def _c3_lora_module(torch, qw, sw, la, lb):
 
 
 def bench_c3(torch, ops, dev) -> dict:
-    """BASELINE configs[2]: FFN at 768p, M=24576, up N=13824 K=5120 and down
+    """BASELINE.json configs[2]: FFN at 768p, M=24576, up N=13824 K=5120 and down
     N=5120 K=13824, e4m3 per-token x per-channel (activation codes in the
     tiled layout), rank-128 LoRA (scale 1.0) added in the GEMM epilogue.
     Times act-quant + LoRA down + scaled GEMM inside steps (as the headline
@@ -216,7 +216,7 @@ def bench_c3(torch, ops, dev) -> dict:
 
 
 def bench_c4(torch, ops, dev) -> dict:
-    """BASELINE configs[3]: skinny M in {16, 64, 128}, K = N = 5120, tiled
+    """BASELINE.json configs[3]: skinny M in {16, 64, 128}, K = N = 5120, tiled
     e4m3 weights, activations quantized into the tiled layout.  Bytes per call
     N*K + 4N + M*K + 4M + 2MN against 8 TB/s; twelve weight copies (315 MB)
     rotate past the Infinity Cache; 48 launches captured in a HIP graph."""
@@ -444,7 +444,7 @@ def bench_f4(torch, ops, dev) -> dict:
 
 
 def bench_c5(torch, ops, dev) -> dict:
-    """BASELINE configs[4]: int8 W8A8 at 1080p, M=40960, K=N=5120: per-token
+    """BASELINE.json configs[4]: int8 W8A8 at 1080p, M=40960, K=N=5120: per-token
     int8 act quant (vLLM formula) + int32-exact GEMM with fused dequant.  The
     GEMM is timed inside steps (act-quant, then GEMM) and back to back; the
     act-quant back to back (its HBM figure)."""
@@ -619,7 +619,7 @@ def bench_ceilings(torch, ops, dev) -> dict:
 
 def cpu_baseline_per_config(torch, budget_s: float = 1.0) -> dict:
     """The reference's formulas on the host (oracle/torch_path.py) for each
-    BASELINE config, on a bounded row sample (synthetic inputs of the config's
+    BASELINE.json config, on a bounded row sample (synthetic inputs of the config's
     shape and distribution): act-quant (3MK + 4M bytes), the quantized GEMM
     (2MNK; FP8 dequant-then-matmul, which dequantizes the weight every call as
     that path does, int8 torch._int_mm then the epilogue), LoRA (c3) and the
@@ -839,7 +839,7 @@ def main() -> int:
         "dtype": "fp8_e4m3fn (fp32 accumulate, bf16 out)",
         "data": "synthetic (seed 0; N(0,1) activations with 1% channels x15; N(0,0.02) weights)",
         "config": {
-            "workload": "c2: DiT QKV projection, 480p streaming chunk (BASELINE configs[1])",
+            "workload": "c2: DiT QKV projection, 480p streaming chunk (BASELINE.json configs[1])",
             "M_tokens": M, "K": K, "N": N,
             "act_quant": "per-token dynamic e4m3fn, codes in the tiled layout",
             "weight_quant": "per-output-channel e4m3fn (offline, tiled layout)",

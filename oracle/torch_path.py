@@ -18,7 +18,7 @@ every bf16 value.
 * ``quantize_act_int8_vllm`` vLLM's dynamic per-token int8 (H3/inference/w8a8.py:178)
 * ``int8_linear``            torch._int_mm then s_a * (s_w * float(acc))
 * ``fp8_linear``             dequant-then-matmul F.linear(q_a.float()*s_a,
-                             q_w.float()*s_w, bias) -> bf16 (BASELINE CPU plan)
+                             q_w.float()*s_w, bias) -> bf16 (the CPU baseline)
 * ``lora_update``            H3/inference/lora_checkpoint.py:196-205
 """
 

@@ -6,7 +6,7 @@ FL/distributed/linear.py:16-181:
 * ``_module_linear(module, inputs, bias)`` (H3/distributed/linear.py:15-33)
   dispatches on module attributes: ``_cutlass_w8a8_weight_scale`` -> int8
   W8A8, ``_fp8_w8a8_weight_scale`` -> per-token x per-channel FP8 W8A8 (the
-  BASELINE format; no counterpart in the reference), ``_fp8_weight_scale`` ->
+  BASELINE.json format; no counterpart in the reference), ``_fp8_weight_scale`` ->
   per-tensor FP8 (FL), otherwise ``F.linear``.
 * ``_linear(...)`` keeps FL's functional signature (FL/distributed/linear.py:50-101)
   including the "cannot combine" error.

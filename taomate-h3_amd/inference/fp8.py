@@ -332,7 +332,7 @@ def synchronize_h3_block_fp8_activation_scales_(torch: Any, transformer: Any, *,
 def quantize_h3_block_linears_fp8_w8a8_(torch: Any, transformer: Any, *, policy: str | None = None) -> dict:
     """Per-output-channel e4m3fn weights + dynamic per-token e4m3fn activations
     for the selected block linears (no counterpart in the reference; the
-    format of the BASELINE FP8 W8A8 configurations).  Bias is kept (bf16) and
+    format of the BASELINE.json FP8 W8A8 configurations).  Bias is kept (bf16) and
     fused into the GEMM epilogue.  Weights with N % 16 == 0 and K % 128 == 0
     are stored in the tiled layout (``ops.is_tiled(weight)``)."""
     candidates = _block_candidates(transformer, (".attn.qkv_proj", ".attn.out_proj", ".mlp.fc1", ".mlp.fc2"))

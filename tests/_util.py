@@ -22,7 +22,7 @@ def from_bits16(b: np.ndarray) -> torch.Tensor:
 
 def activations(m: int, k: int, seed: int = 0, outlier_channels: int = 0, outlier_scale: float = 20.0,
                 student_t: bool = False) -> torch.Tensor:
-    """N(0,1) activations with a few seeded outlier channels."""
+    """N(0,1) activations with a few seeded outlier channels (the BASELINE.json configurations)."""
     gen = torch.Generator().manual_seed(seed)
     x = torch.randn(m, k, generator=gen)
     if outlier_channels:

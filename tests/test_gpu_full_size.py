@@ -1,4 +1,4 @@
-"""The BASELINE configurations at their own sizes, on the kernels the bench times.
+"""The BASELINE.json configurations at their own sizes, on the kernels the bench times.
 
 Every GEMM here runs at full size on the GPU; the CPU oracle checks a
 stratified set of output rows: at least one row of every 256-row tile-row,

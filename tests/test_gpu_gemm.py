@@ -180,7 +180,7 @@ def test_fp8_per_tensor_scales(ops, oracle, device):
 
 
 def test_fp8_c2_shape_sampled_rows(ops, oracle, device):
-    """BASELINE c2 (QKV 480p: M=8192, K=5120, N=15360): full GPU GEMM, 48
+    """BASELINE.json c2 (QKV 480p: M=8192, K=5120, N=15360): full GPU GEMM, 48
     seeded rows checked against the exact oracle across all N columns."""
     out, rqa, rsa, rqw, rsw, bb = _fp8_case(ops, oracle, device, 8192, 15360, 5120, seed=0, bias=True)
     rows = np.sort(np.random.default_rng(0).choice(8192, 48, replace=False))

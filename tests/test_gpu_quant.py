@@ -2,7 +2,7 @@
 
 Covers the per-row kernel (vector path and general path), the per-tensor
 two-pass kernel, every bf16 value through the e4m3fn conversion, zero rows,
-signed zeros, ragged K, row tails and the BASELINE full-size activations."""
+signed zeros, ragged K, row tails and the BASELINE.json full-size activations."""
 
 from __future__ import annotations
 
@@ -259,7 +259,7 @@ def test_tensor_e4m3_3d_input(ops, oracle, device):
     ("c5_int8_1080p", 40960, 5120, "int8", "rcp", True),
 ])
 def test_full_size_activations(ops, oracle, device, name, m, k, fmt, rounding, student):
-    """BASELINE activation shapes (c3 down: 2048 of its 24576 rows), bit-exact."""
+    """BASELINE.json activation shapes (c3 down: 2048 of its 24576 rows), bit-exact."""
     print(f"full-size act quant {name}", flush=True)
     x = activations(m, k, seed=0, outlier_channels=max(1, k // 100), outlier_scale=15.0, student_t=student)
     _check_rows(ops, oracle, x, device, fmt, rounding)
