@@ -185,3 +185,39 @@ def test_more_than_64_rows_per_wave(ops, oracle, device):
     table indices of its next 64 rows; random indices over five table rows
     make a misplaced index visible."""
     _check(ops, oracle, device, 64 * 4096 + 37, 8, "int8", "rcp", resid=True, t=5, seed=11)
+
+
+@pytest.mark.parametrize("fmt,rounding", [("e4m3", "div"), ("int8", "rcp")])
+def test_rows_with_infinities_and_nans(ops, oracle, device, fmt, rounding):
+    """Rows holding an infinity, a NaN, values whose squares overflow the sum
+    (so rs = 0), and an all-zero row (rs = 1/sqrt(eps)): the normalized,
+    modulated rows, codes and scales follow the oracle's IEEE operations;
+    NaNs are compared as NaN (their payload and sign are not fixed)."""
+    rows, cols, eps = 6, 1024, 1e-6
+    x = activations(rows, cols, seed=31)
+    x[0, 5] = float("inf")
+    x[1, 9] = float("nan")
+    x[2, :] = 3.0e38
+    x[3, :] = 0.0
+    x[5, 7] = float("-inf")
+    weight, scale, shift, _ = _tables(2, cols, 32)
+    idx = torch.tensor([0, 1, 0, 1, 0, 1], dtype=torch.int64)
+    f, r = _fmt(ops, fmt, rounding)
+    print(f"norm_quant special rows {fmt}/{rounding}", flush=True)
+    out, codes, scales = ops.norm_modulate_quant(x.to(device), weight.to(device), scale.to(device),
+                                                 shift.to(device), idx.to(device), eps, fmt=f, rounding=r, out=True)
+    torch.cuda.synchronize()
+    ry, _ = oracle.rms_norm_modulate(bits16(x), bits16(weight), bits16(scale), bits16(shift), idx.numpy(), eps)
+    got = bits16(out)
+    nan_y = (ry & 0x7FFF) > 0x7F80
+    np.testing.assert_array_equal((got & 0x7FFF) > 0x7F80, nan_y)
+    np.testing.assert_array_equal(np.where(nan_y, 0, got), np.where(nan_y, 0, ry))
+    rq, rs = oracle.quant_rows(ry, fmt, rounding)
+    got_s = scales.cpu().numpy().ravel()
+    np.testing.assert_array_equal(np.isnan(got_s), np.isnan(rs))
+    np.testing.assert_array_equal(got_s[~np.isnan(rs)], rs[~np.isnan(rs)])
+    gq, wq = bits8(codes), rq.view(np.uint8)
+    nan_q = ((wq & 0x7F) == 0x7F) if fmt == "e4m3" else np.zeros(wq.shape, dtype=bool)
+    if fmt == "e4m3":
+        np.testing.assert_array_equal((gq & 0x7F) == 0x7F, nan_q)
+    np.testing.assert_array_equal(np.where(nan_q, 0, gq), np.where(nan_q, 0, wq))
