@@ -335,3 +335,50 @@ def test_lora_down_split_over_k(ops, oracle, device, m, k, rank):
     rc = _lib.lib().h3q_lora_down_ws(xg.data_ptr(), k, lag.data_ptr(), k, out.data_ptr(), rank, m, k, rank,
                                      ws.data_ptr(), need - 16, None)
     assert rc != 0 and b"workspace" in _lib.lib().h3q_last_error()
+
+
+@pytest.mark.parametrize("m,a_tiled", [(512, False), (512, True), (64, False), (16, True)])
+def test_fp8_nan_codes_propagate(ops, device, m, a_tiled):
+    """A NaN code (0x7F / 0xFF in e4m3fn) in an activation row makes exactly
+    that output row NaN, and one in a weight row exactly that output column,
+    as exact arithmetic (and the reference's torch._scaled_mm) gives; every
+    other element equals the NaN-free call bit for bit.  Large M (four-wave
+    kernel, row-major or tiled activations) and M <= 128 (weight-streaming
+    kernel)."""
+    from _util import to_tiled
+
+    k, n = 1024, 768
+    gen = torch.Generator().manual_seed(m + 1)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(device)
+    print(f"fp8 nan codes m={m} a_tiled={a_tiled}", flush=True)
+    qw, sw = ops.quant_rows_tiled(w, ops.FMT_E4M3FN)
+    qa, sa = ops.quant_rows(x, ops.FMT_E4M3FN)
+
+    def run(a_codes, w_codes):
+        a = a_codes
+        if a_tiled:
+            rows = ((m + 15) // 16) * 16
+            pad = torch.zeros(rows, k, dtype=torch.uint8)
+            pad[:m] = a_codes.view(torch.uint8).cpu()
+            a = torch.from_numpy(to_tiled(pad.numpy())).view(torch.float8_e4m3fn).to(device)
+        return ops.scaled_mm(a, w_codes, sa.reshape(-1), sw.reshape(-1), b_tiled=True, a_tiled=a_tiled, m=m)
+
+    base = run(qa, qw)
+    qa_nan = qa.clone()
+    qa_nan.view(torch.uint8)[3, 17] = 0x7F
+    qa_nan.view(torch.uint8)[m - 1, 100] = 0xFF
+    # the weight is tiled: a NaN in weight row 10 at k = 5 (block 0, row 10 of
+    # its 16-row block, k-step 0) sits at byte 16 * 10 + 5 of the first tile
+    qw_nan = qw.clone()
+    qw_nan.view(torch.uint8).view(-1)[16 * 10 + 5] = 0x7F
+    out = run(qa_nan, qw_nan)
+    torch.cuda.synchronize()
+    o, b = out.float().cpu(), base.float().cpu()
+    nan = torch.isnan(o)
+    want = torch.zeros(m, n, dtype=torch.bool)
+    want[3, :] = True
+    want[m - 1, :] = True
+    want[:, 10] = True
+    assert torch.equal(nan, want)
+    assert torch.equal(o[~want], b[~want])
