@@ -73,6 +73,28 @@ def test_codes_only_output_only_and_strided_rows(ops, oracle, device):
     np.testing.assert_array_equal(bits8(codes), rq)
 
 
+def test_table_form_strided_rows(ops, oracle, device):
+    """1030 rows (the table form) read from a wider buffer and written into
+    row slices of wider output and code buffers: bit-exact."""
+    half = 1024
+    wide = _inputs(1030, 2 * half + 64, 8)
+    x = wide[:, :2 * half]
+    out_wide = torch.zeros(1030, half + 32, device=device, dtype=torch.bfloat16)
+    codes_wide = torch.zeros(1030, half + 64, device=device, dtype=torch.float8_e4m3fn)
+    scales = torch.empty(1030, 1, device=device, dtype=torch.float32)
+    print("swiglu table form, strided rows", flush=True)
+    ops.swiglu_quant(wide.to(device)[:, :2 * half], fmt=ops.FMT_E4M3FN, out=out_wide[:, :half],
+                     codes=codes_wide[:, :half], scales=scales)
+    torch.cuda.synchronize()
+    ry = oracle.swiglu(bits16(x))
+    np.testing.assert_array_equal(bits16(out_wide[:, :half]), ry)
+    assert not bits16(out_wide[:, half:]).any()
+    rq, rs = oracle.quant_rows(ry, "e4m3", "div")
+    np.testing.assert_array_equal(bits8(codes_wide[:, :half]), rq)
+    assert not bits8(codes_wide[:, half:]).any()
+    np.testing.assert_array_equal(scales.cpu().numpy().ravel(), rs)
+
+
 def test_special_values(ops, oracle, device):
     """Zero, huge and infinite gates, gates whose exp overflows, -0 and
     products in the binary32 subnormal range: bit-exact against the oracle."""
